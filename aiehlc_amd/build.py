@@ -1,0 +1,87 @@
+"""Build step for the miaie HIP library (gfx950 only).
+
+Compiles every aiehlc_amd/csrc/*.hip translation unit with hipcc for gfx950
+and links them into aiehlc_amd/lib/libmiaie.so, then builds the C++ harness
+programs in aiehlc_amd/harness/ against it.  Runs on a machine without a GPU
+(hipcc cross-compiles).
+
+Flags: -O3, C++17, hidden visibility (only the MIAIE_API symbols of
+include/miaie.h are exported), and packed-FP32 instruction selection turned
+off (`-Xclang -target-feature -Xclang -packed-fp32-ops`).
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
+LIBDIR = os.path.join(HERE, "lib")
+LIB = os.path.join(LIBDIR, "libmiaie.so")
+HARNESS = os.path.join(HERE, "harness")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+    f"-I{os.path.join(ROOT, 'include')}",
+]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    out = (r.stdout + r.stderr).strip()
+    # hipcc's host pass does not know the packed-fp32 feature: harmless, drop it
+    lines = [l for l in out.splitlines() if "packed-fp32-ops" not in l and l.strip()
+             and "not a recognized feature for this target" not in l]
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n" + "\n".join(lines))
+    if lines and verbose:
+        print("\n".join(lines), flush=True)
+
+
+def sources() -> list[str]:
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    os.makedirs(LIBDIR, exist_ok=True)
+    srcs = sources()
+    objs = [os.path.join(OBJ, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    jobs = jobs or min(8, len(srcs))
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-c", s, "-o", o], verbose) for s, o in zip(srcs, objs)]
+        for f in futs:
+            f.result()
+    tmp = LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    os.replace(tmp, LIB)
+    build_harness(verbose)
+    return LIB
+
+
+def build_harness(verbose: bool = False) -> None:
+    if not os.path.isdir(HARNESS):
+        return
+    for f in sorted(os.listdir(HARNESS)):
+        if not f.endswith(".cpp"):
+            continue
+        exe = os.path.join(HARNESS, f[:-4])
+        cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}",
+               os.path.join(HARNESS, f), "-o", exe + ".tmp", f"-L{LIBDIR}", "-lmiaie",
+               "-Wl,-rpath,$ORIGIN/../lib"]
+        _run(cmd, verbose)
+        os.replace(exe + ".tmp", exe)
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

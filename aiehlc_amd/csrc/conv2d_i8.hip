@@ -1,0 +1,203 @@
+// int8 conv2d (NHWC x OHWI -> NHWC) with a per-output-channel requantize
+// epilogue, as an im2col-free implicit GEMM on gfx950 MFMA.
+//
+// The reference's conv exists only as the generated control code of an AIE
+// graph (thirdparty/adf/aie_control.cpp:854-1524: 8 `conv` kernels with
+// ping/pong activation windows); no kernel source ships.  Semantics are the
+// benchmark's: zero padding, stride, int32 accumulation, then
+// y = sat_int8((acc + 2^(s_c-1)) >> s_c) per output channel c.
+//
+// GEMM view: rows = output pixels (n, ho, wo), columns = output channels,
+// k = (r, s, ci).  A workgroup owns 64 consecutive pixels x 64 channels.
+// Each of its 4 waves takes every 4th k-step of 32 (one (r, s, ci-block)),
+// loading X and W fragments straight from global memory in MFMA operand
+// layout (W rows are k-contiguous in OHWI; X pixels are ci-contiguous in
+// NHWC), so no im2col buffer and no LDS staging of the operands.  The four
+// partial 64x64 int32 tiles are summed through LDS, requantized and written
+// as one contiguous 4 KiB run of NHWC output.
+#include "miaie_internal.hpp"
+
+namespace {
+
+__device__ __forceinline__ int requant1(int acc, int s) {
+  int q = s ? (acc >> s) + ((acc >> (s - 1)) & 1) : acc;
+  return min(max(q, -128), 127);
+}
+
+constexpr int PIX = 64;    // pixels per workgroup
+constexpr int COB = 64;    // output channels per workgroup
+constexpr int BATCH = 6;   // k-steps whose fragments are in flight per wave
+
+__global__ __launch_bounds__(256) void conv2d_i8_igemm(
+    const int8_t* __restrict__ X, const int8_t* __restrict__ W, const uint8_t* __restrict__ shifts,
+    int8_t* __restrict__ Y, int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad,
+    int Ho, int Wo) {
+  __shared__ __attribute__((aligned(16))) int32_t part[4][PIX * COB];  // 64 KiB
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int P = N * Ho * Wo;
+  const int p0 = blockIdx.x * PIX;
+  const int co0 = blockIdx.y * COB;
+
+  // the two pixels this lane feeds (one per 32-pixel block)
+  int pn[2], phb[2], pwb[2];
+  bool pvalid[2];
+#pragma unroll
+  for (int pb = 0; pb < 2; ++pb) {
+    const int p = p0 + 32 * pb + fr;
+    pvalid[pb] = p < P;
+    const int pp = pvalid[pb] ? p : 0;
+    const int wo = pp % Wo;
+    const int t = pp / Wo;
+    const int ho = t % Ho;
+    pn[pb] = t / Ho;
+    phb[pb] = ho * stride - pad;
+    pwb[pb] = wo * stride - pad;
+  }
+  const int KW = R * S * Cin;  // weight row length (OHWI)
+  const int8_t* wrow[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) wrow[cb] = W + (size_t)(co0 + 32 * cb + fr) * KW + 16 * fh;
+
+  const int CBI = Cin / 32;
+  const int T = R * S * CBI;
+
+  v16i acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = v16i{0};
+
+  for (int t0 = wave; t0 < T; t0 += 4 * BATCH) {
+    v4i xf[BATCH][2], wf[BATCH][2];
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int t = t0 + 4 * u;
+      if (t < T) {
+        const int rs = t / CBI, cib = t - rs * CBI;
+        const int r = rs / S, s = rs - r * S;
+        const int koff = rs * Cin + cib * 32;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) wf[u][cb] = *reinterpret_cast<const v4i*>(wrow[cb] + koff);
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+          const int hi = phb[pb] + r, wi = pwb[pb] + s;
+          const bool ok = pvalid[pb] && hi >= 0 && hi < H && wi >= 0 && wi < Wd;
+          const int8_t* src = X + (((size_t)pn[pb] * H + hi) * Wd + wi) * Cin + cib * 32 + 16 * fh;
+          xf[u][pb] = ok ? *reinterpret_cast<const v4i*>(src) : v4i{0};
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      if (t0 + 4 * u < T) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+          for (int pb = 0; pb < 2; ++pb)
+            acc[cb][pb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[u][cb], xf[u][pb], acc[cb][pb], 0, 0, 0);
+      }
+    }
+  }
+
+  // acc[cb][pb][4g + t]: channel co = 32cb + 8g + 4*(lane/32) + t, pixel p = 32pb + lane%32.
+  // Partial tile layout: [pixel][16-byte channel quad, XOR pixel%16].
+  int32_t* mine = part[wave];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int p = 32 * pb + fr;
+        const int cq = (32 * cb + 8 * g + 4 * fh) >> 2;
+        v4i v = {acc[cb][pb][4 * g], acc[cb][pb][4 * g + 1], acc[cb][pb][4 * g + 2], acc[cb][pb][4 * g + 3]};
+        *reinterpret_cast<v4i*>(mine + p * COB + ((cq ^ (p & 15)) << 2)) = v;
+      }
+  __syncthreads();
+
+  // thread -> pixel tid/4, channels 16*(tid%4) .. +16
+  const int p = tid >> 2, c16 = (tid & 3) * 16;
+  if (p0 + p >= P) return;
+  int sum[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int cq = (c16 >> 2) + q;
+    v4i s = v4i{0};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) s += *reinterpret_cast<const v4i*>(part[w] + p * COB + ((cq ^ (p & 15)) << 2));
+    sum[4 * q] = s[0];
+    sum[4 * q + 1] = s[1];
+    sum[4 * q + 2] = s[2];
+    sum[4 * q + 3] = s[3];
+  }
+  uint32_t out[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int c = co0 + c16 + 4 * q + t;
+      v |= (uint32_t)(requant1(sum[4 * q + t], shifts[c]) & 0xFF) << (8 * t);
+    }
+    out[q] = v;
+  }
+  *reinterpret_cast<uint4*>(Y + (size_t)(p0 + p) * Cout + co0 + c16) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// Any-shape fallback: one thread per output element.
+__global__ __launch_bounds__(256) void conv2d_i8_direct(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
+                                                        const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
+                                                        int N, int H, int Wd, int Cin, int Cout, int R, int S,
+                                                        int stride, int pad, int Ho, int Wo) {
+  const size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  const size_t total = (size_t)N * Ho * Wo * Cout;
+  if (idx >= total) return;
+  const int co = (int)(idx % Cout);
+  size_t t = idx / Cout;
+  const int wo = (int)(t % Wo);
+  t /= Wo;
+  const int ho = (int)(t % Ho);
+  const int n = (int)(t / Ho);
+  uint32_t acc = 0;
+  for (int r = 0; r < R; ++r) {
+    const int hi = ho * stride + r - pad;
+    if (hi < 0 || hi >= H) continue;
+    for (int s = 0; s < S; ++s) {
+      const int wi = wo * stride + s - pad;
+      if (wi < 0 || wi >= Wd) continue;
+      const int8_t* x = X + (((size_t)n * H + hi) * Wd + wi) * Cin;
+      const int8_t* w = W + (((size_t)co * R + r) * S + s) * Cin;
+      for (int ci = 0; ci < Cin; ++ci) acc += (uint32_t)((int)x[ci] * (int)w[ci]);
+    }
+  }
+  Y[idx] = (int8_t)requant1((int)acc, shifts[co]);
+}
+
+}  // namespace
+
+namespace miaie {
+
+int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y,
+                     int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad) {
+  const int Ho = (H + 2 * pad - R) / stride + 1;
+  const int Wo = (Wd + 2 * pad - S) / stride + 1;
+  const size_t P = (size_t)N * Ho * Wo;
+  const bool fast = Cin % 32 == 0 && Cout % COB == 0 && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) &&
+                    P < ((size_t)1 << 31) && (P + PIX - 1) / PIX < ((size_t)1 << 31);
+  if (fast) {
+    dim3 grid((unsigned)((P + PIX - 1) / PIX), Cout / COB);
+    hipLaunchKernelGGL(conv2d_i8_igemm, grid, dim3(256), 0, ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout,
+                       R, S, stride, pad, Ho, Wo);
+    return check_launch(ctx, "conv2d_i8_igemm");
+  }
+  const size_t total = P * Cout;
+  const size_t blocks = (total + 255) / 256;
+  if (blocks >= ((size_t)1 << 31)) return fail(ctx, MIAIE_EINVAL, "conv2d: output too large for the direct kernel");
+  hipLaunchKernelGGL(conv2d_i8_direct, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, X, W, shifts, Y, N, H,
+                     Wd, Cin, Cout, R, S, stride, pad, Ho, Wo);
+  return check_launch(ctx, "conv2d_i8_direct");
+}
+
+}  // namespace miaie

@@ -1,0 +1,57 @@
+// Internal declarations shared by the miaie HIP translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "../../include/miaie.h"
+
+struct miaie_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  hipEvent_t done = nullptr;  // recorded by miaie_wait
+  char err[512] = {0};
+};
+
+namespace miaie {
+
+// Record an error message on the context (printf-style) and return `code`.
+int fail(miaie_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+
+// Map a HIP error to MIAIE_EHIP with a message naming the call.
+int hip_fail(miaie_ctx* ctx, hipError_t e, const char* what);
+
+// Every entry point starts with this: non-null context, its device current.
+int enter(miaie_ctx* ctx);
+
+// Check the launch that was just queued.
+int check_launch(miaie_ctx* ctx, const char* kernel);
+
+__host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// ---- kernel launchers implemented in the kernel translation units ----
+int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
+                   int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu);
+int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float* C, int M, int N,
+                     int K);
+int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts,
+                     int8_t* Y, int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride,
+                     int pad);
+
+}  // namespace miaie
+
+// Vector types used by the MFMA builtins.
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+#define MIAIE_CHECK_NOT_NULL(ctx, p)                                              \
+  do {                                                                          \
+    if ((p) == nullptr) return miaie::fail((ctx), MIAIE_EINVAL, "%s: " #p " is NULL", __func__); \
+  } while (0)

@@ -1,0 +1,288 @@
+// miaie runtime: context, device memory, copies, waits, synthetic fills.
+//
+// These entry points stand in for the aie-rt host calls the reference
+// harnesses make (example/perf/aieml_perf.cc:256-328,
+// example/matrixmultiply/aieml_mm.cc:108-249): configuration and partition
+// set-up become a context bound to one HIP device and stream; MemAllocate
+// and MoveData become hipMalloc and stream-ordered copies; Run becomes an
+// asynchronous kernel launch; CoreWaitForDone becomes an event wait with a
+// deadline.
+#include <time.h>
+
+#include <cstring>
+
+#include "miaie_internal.hpp"
+
+namespace {
+thread_local char g_init_err[512] = {0};
+}
+
+namespace miaie {
+
+int fail(miaie_ctx* ctx, int code, const char* fmt, ...) {
+  char* buf = ctx ? ctx->err : g_init_err;
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, 512, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(miaie_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, e == hipErrorOutOfMemory ? MIAIE_ENOMEM : MIAIE_EHIP, "%s: %s (%s)", what,
+              hipGetErrorString(e), hipGetErrorName(e));
+}
+
+int enter(miaie_ctx* ctx) {
+  if (!ctx) return fail(nullptr, MIAIE_EINVAL, "context is NULL");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  return MIAIE_OK;
+}
+
+int check_launch(miaie_ctx* ctx, const char* kernel) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(ctx, e, kernel);
+  return MIAIE_OK;
+}
+
+}  // namespace miaie
+
+using namespace miaie;
+
+// ---------------------------------------------------------------- kernels
+namespace {
+
+constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
+
+__host__ __device__ inline uint64_t sm64_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// Streaming copy: 16-byte vectors for the aligned body, bytes for the rest.
+__global__ __launch_bounds__(256) void copy_kernel(v4i* __restrict__ dst,
+                                                   const v4i* __restrict__ src, size_t nvec,
+                                                   uint8_t* __restrict__ dst_tail,
+                                                   const uint8_t* __restrict__ src_tail,
+                                                   size_t ntail) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < nvec; i += stride) dst[i] = __builtin_nontemporal_load(src + i);
+  size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (t < ntail) dst_tail[t] = src_tail[t];
+}
+
+// 16 seeded int8 values per thread.
+__global__ __launch_bounds__(256) void fill_i8_kernel(int8_t* __restrict__ dst, size_t n,
+                                                      uint64_t state0) {
+  size_t base = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) * 16;
+  if (base >= n) return;
+  if (base + 16 <= n) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        uint64_t r = sm64_mix(state0 + (base + 4 * q + b + 1) * kGamma);
+        v |= (uint32_t)(r >> 56) << (8 * b);
+      }
+      w[q] = v;
+    }
+    *reinterpret_cast<uint4*>(dst + base) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    for (size_t i = base; i < n; ++i) dst[i] = (int8_t)(uint8_t)(sm64_mix(state0 + (i + 1) * kGamma) >> 56);
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- context
+extern "C" int miaie_init_on_stream(miaie_ctx** out, int device, void* stream) {
+  if (!out) return fail(nullptr, MIAIE_EINVAL, "miaie_init: ctx out-pointer is NULL");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "hipGetDeviceCount");
+  if (device < 0 || device >= count)
+    return fail(nullptr, MIAIE_EINVAL, "miaie_init: device %d out of range [0, %d)", device, count);
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, MIAIE_EUNSUPPORTED, "miaie is built for gfx950 only; device %d is %s", device,
+                prop.gcnArchName);
+  miaie_ctx* ctx = new (std::nothrow) miaie_ctx();
+  if (!ctx) return fail(nullptr, MIAIE_ENOMEM, "miaie_init: host allocation failed");
+  ctx->device = device;
+  if (stream) {
+    ctx->stream = static_cast<hipStream_t>(stream);
+  } else {
+    ctx->stream = nullptr;
+  }
+  e = hipEventCreateWithFlags(&ctx->done, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    int rc = hip_fail(nullptr, e, "hipEventCreate");
+    delete ctx;
+    return rc;
+  }
+  *out = ctx;
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_init(miaie_ctx** out, int device) {
+  int rc = miaie_init_on_stream(out, device, nullptr);
+  if (rc != MIAIE_OK) return rc;
+  miaie_ctx* ctx = *out;
+  hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    rc = hip_fail(nullptr, e, "hipStreamCreate");
+    (void)hipEventDestroy(ctx->done);
+    delete ctx;
+    *out = nullptr;
+    return rc;
+  }
+  ctx->own_stream = true;
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_finish(miaie_ctx* ctx) {
+  if (!ctx) return MIAIE_OK;
+  int rc = MIAIE_OK;
+  (void)hipSetDevice(ctx->device);
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) rc = MIAIE_EHIP;
+  if (ctx->done) (void)hipEventDestroy(ctx->done);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return rc;
+}
+
+extern "C" const char* miaie_last_error_string(const miaie_ctx* ctx) {
+  return ctx ? ctx->err : g_init_err;
+}
+
+extern "C" int miaie_get_stream(miaie_ctx* ctx, void** stream) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  MIAIE_CHECK_NOT_NULL(ctx, stream);
+  *stream = ctx->stream;
+  return MIAIE_OK;
+}
+
+// ---------------------------------------------------------------- memory
+extern "C" int miaie_alloc(miaie_ctx* ctx, size_t bytes, void** dev_ptr) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  MIAIE_CHECK_NOT_NULL(ctx, dev_ptr);
+  *dev_ptr = nullptr;
+  if (bytes == 0) return fail(ctx, MIAIE_EINVAL, "miaie_alloc: zero bytes");
+  hipError_t e = hipMalloc(dev_ptr, bytes);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc");
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_free(miaie_ctx* ctx, void* dev_ptr) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (!dev_ptr) return MIAIE_OK;
+  hipError_t e = hipFree(dev_ptr);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_copy_h2d(miaie_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (bytes == 0) return MIAIE_OK;
+  MIAIE_CHECK_NOT_NULL(ctx, dst);
+  MIAIE_CHECK_NOT_NULL(ctx, src);
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipMemcpyAsync(H2D)");
+  e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_copy_d2h(miaie_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (bytes == 0) return MIAIE_OK;
+  MIAIE_CHECK_NOT_NULL(ctx, dst);
+  MIAIE_CHECK_NOT_NULL(ctx, src);
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipMemcpyAsync(D2H)");
+  e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_copy_d2d(miaie_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (bytes == 0) return MIAIE_OK;
+  MIAIE_CHECK_NOT_NULL(ctx, dst);
+  MIAIE_CHECK_NOT_NULL(ctx, src);
+  const bool vec_ok = aligned(dst, 16) && aligned(src, 16);
+  const size_t nvec = vec_ok ? bytes / 16 : 0;
+  const size_t done = nvec * 16;
+  const size_t ntail = bytes - done;
+  if (ntail > (size_t)1 << 30) return fail(ctx, MIAIE_EINVAL, "miaie_copy_d2d: unaligned copies are limited to 1 GiB");
+  size_t threads_needed = nvec > ntail ? nvec : ntail;
+  size_t blocks = (threads_needed + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < (ntail + 255) / 256) blocks = (ntail + 255) / 256;
+  if (blocks == 0) blocks = 1;
+  hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream,
+                     static_cast<v4i*>(dst), static_cast<const v4i*>(src), nvec,
+                     static_cast<uint8_t*>(dst) + done, static_cast<const uint8_t*>(src) + done, ntail);
+  return check_launch(ctx, "copy_kernel");
+}
+
+// ---------------------------------------------------------------- waits
+extern "C" int miaie_wait(miaie_ctx* ctx, int timeout_ms) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  hipError_t e = hipEventRecord(ctx->done, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
+  if (timeout_ms < 0) {
+    e = hipEventSynchronize(ctx->done);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipEventSynchronize");
+    return MIAIE_OK;
+  }
+  timespec t0;
+  clock_gettime(CLOCK_MONOTONIC, &t0);
+  for (;;) {
+    e = hipEventQuery(ctx->done);
+    if (e == hipSuccess) return MIAIE_OK;
+    if (e != hipErrorNotReady) return hip_fail(ctx, e, "hipEventQuery");
+    timespec t1;
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    double ms = (t1.tv_sec - t0.tv_sec) * 1e3 + (t1.tv_nsec - t0.tv_nsec) * 1e-6;
+    if (ms >= timeout_ms)
+      return fail(ctx, MIAIE_ETIMEDOUT, "miaie_wait: stream not drained after %d ms", timeout_ms);
+    timespec nap = {0, 20000};  // 20 us
+    nanosleep(&nap, nullptr);
+  }
+}
+
+// ---------------------------------------------------------------- synthetic data
+extern "C" int miaie_fill_i8(miaie_ctx* ctx, int8_t* dst, size_t n, uint64_t tensor_id) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (n == 0) return MIAIE_OK;
+  MIAIE_CHECK_NOT_NULL(ctx, dst);
+  if (!aligned(dst, 16)) return fail(ctx, MIAIE_EINVAL, "miaie_fill_i8: dst must be 16-byte aligned");
+  const uint64_t state0 = sm64_mix(0x5EED0000ull + tensor_id + kGamma);
+  const size_t threads = (n + 15) / 16;
+  const size_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return fail(ctx, MIAIE_EINVAL, "miaie_fill_i8: n too large");
+  hipLaunchKernelGGL(fill_i8_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, dst, n, state0);
+  return check_launch(ctx, "fill_i8_kernel");
+}
+
+extern "C" const char* miaie_version(void) { return "miaie 0.1 (gfx950)"; }

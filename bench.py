@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Benchmark: int8 GEMM + requant at M=N=K=4096 on one MI355X.
+
+One step = one miaie_gemm_i8_rq launch (A 4096x4096 int8 NN B 4096x4096 int8,
+int32 accumulate, Y = sat_int8((acc + 2^9) >> 10)) over inputs already
+resident in HBM.  W untimed warm-up steps, then K timed steps bracketed by a
+stream drain on both sides and HIP events on the stream the kernel is
+launched on.  Prints ONE JSON line.
+
+Extras in the same line (not the headline): the 3x3 int8 conv2d of config 4
+(GOPS), the bf16 8192^3 GEMM of config 3 and the int8 MLP of config 5.
+
+cpu_baseline: the reference's CPU golden loop (i-j-k, int32 accumulate, B in
+the reference's [N][K] layout: example/matrixmultiply/aieml_mm.cc:217-223),
+restated in oracle/miaie_oracle.c, timed on this host on a row slab of the
+same 4096^3 problem.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, TOP/s
+PEAK_BF16_TFLOPS = 2500.0    # dense bf16
+PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_rq_4096_traffic.json")
+
+
+class HipTimer:
+    """hipEvent pair on a given stream (the miaie context's stream)."""
+
+    def __init__(self, stream: int):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.stream = C.c_void_p(stream)
+        self.e0, self.e1 = C.c_void_p(), C.c_void_p()
+        for e in (self.e0, self.e1):
+            self._ok(self.hip.hipEventCreate(C.byref(e)), "hipEventCreate")
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    def start(self):
+        self._ok(self.hip.hipEventRecord(self.e0, self.stream), "hipEventRecord")
+
+    def stop_ms(self) -> float:
+        self._ok(self.hip.hipEventRecord(self.e1, self.stream), "hipEventRecord")
+        self._ok(self.hip.hipEventSynchronize(self.e1), "hipEventSynchronize")
+        ms = C.c_float()
+        self._ok(self.hip.hipEventElapsedTime(C.byref(ms), self.e0, self.e1), "hipEventElapsedTime")
+        return float(ms.value)
+
+
+def timed(ctx, timer, fn, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn()
+    ctx.wait(120_000)
+    timer.start()
+    for _ in range(steps):
+        fn()
+    ms = timer.stop_ms()
+    ctx.wait(120_000)
+    return ms / steps
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """Reference golden loop on the host: rows slab of the 4096^3 problem."""
+    import oracle
+    from aiehlc_amd import synth
+
+    M = N = K = 4096
+    threads = min(16, os.cpu_count() or 1)
+    A = synth.int8((M, K), 1)
+    B = synth.int8((K, N), 2)
+    Bt = np.ascontiguousarray(B.T)  # NN -> the reference's [N][K] layout, untimed
+    lib = oracle._lib()
+    Cb = np.zeros((M, N), dtype=np.int32)
+
+    def run(rows, nt):
+        t0 = time.perf_counter()
+        lib.oracle_gemm_i8_nt_rows(A.ctypes.data, Bt.ctypes.data, Cb.ctypes.data, M, N, K, K, K, N, 0, rows, nt)
+        return time.perf_counter() - t0
+
+    probe_rows = threads * 2
+    t = run(probe_rows, threads)
+    rows = int(min(M, max(probe_rows, probe_rows * seconds / max(t, 1e-3))))
+    rows -= rows % threads or 0
+    rows = max(rows, threads)
+    t = run(rows, threads)
+    tops = 2.0 * rows * N * K / t / 1e12
+    t1 = run(8, 1)
+    tops1 = 2.0 * 8 * N * K / t1 / 1e12
+    return {
+        "value": round(tops, 6),
+        "unit": "TOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"rows 0..{rows} of C (of 4096) of the 4096^3 int8 GEMM, reference i-j-k int32 loop "
+                  f"(aieml_mm.cc:217-223) on int8 operands, B transposed to [N][K] untimed, gcc -O2, "
+                  f"OpenMP over rows, {t:.2f}s",
+        "single_thread_value": round(tops1, 6),
+        "requant_in_loop": False,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extras", action="store_true", help="headline workload only")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is described in DESIGN.md and not run", file=sys.stderr)
+        return 2
+
+    import aiehlc_amd as mi
+
+    ctx = mi.Context(0)
+    timer = HipTimer(ctx.stream)
+    M = N = K = 4096
+    dA, dB, dY = ctx.empty((M, K), np.int8), ctx.empty((K, N), np.int8), ctx.empty((M, N), np.int8)
+    ctx.fill_i8(dA, M * K, 1)
+    ctx.fill_i8(dB, K * N, 2)
+    ctx.wait(60_000)
+
+    def step():
+        ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, mi.B_NN)
+
+    ms = timed(ctx, timer, step, args.steps, args.warmup)
+    ops = 2.0 * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    extras = {}
+    if not args.no_extras:
+        # config 4: conv2d 3x3
+        Nb, H, W, Ci, Co = 8, 56, 56, 64, 64
+        dX, dW, dS, dYc = (ctx.empty((Nb, H, W, Ci), np.int8), ctx.empty((Co, 3, 3, Ci), np.int8),
+                           ctx.upload(mi.synth.shifts(Co, 7)), ctx.empty((Nb, H, W, Co), np.int8))
+        ctx.fill_i8(dX, Nb * H * W * Ci, 3)
+        ctx.fill_i8(dW, Co * 9 * Ci, 4)
+        ms_c = timed(ctx, timer, lambda: ctx.conv2d_i8_nhwc(dX, dW, dS, dYc, Nb, H, W, Ci, Co, 3, 3, 1, 1),
+                     max(args.steps, 200), args.warmup)
+        conv_ops = 2.0 * Nb * H * W * Co * Ci * 9
+        conv_bytes = Nb * H * W * Ci + Co * 9 * Ci + Co + Nb * H * W * Co
+        extras["conv2d_3x3"] = {
+            "config": "N=8 H=W=56 Cin=Cout=64 3x3 s1 p1 NHWC/OHWI, per-channel shift",
+            "us_per_step": round(ms_c * 1e3, 3),
+            "gops": round(conv_ops / (ms_c * 1e-3) / 1e9, 1),
+            "alg_GBps": round(conv_bytes / (ms_c * 1e-3) / 1e9, 1),
+            "roof_tops": round(min(PEAK_INT8_TOPS, conv_ops / conv_bytes * PEAK_HBM_GBS / 1e3), 1),
+            "frac_of_roof": round(conv_ops / (ms_c * 1e-3) / 1e12 / min(PEAK_INT8_TOPS, conv_ops / conv_bytes * PEAK_HBM_GBS / 1e3), 4),
+            "note": "events bracket back-to-back launches: includes launch gaps; inputs L2/MALL-hot",
+        }
+        for b in (dX, dW, dS, dYc):
+            b.free()
+        # config 3: bf16 8192^3
+        Mb = 8192
+        dAb, dBb, dCb = ctx.empty((Mb, Mb), np.uint16), ctx.empty((Mb, Mb), np.uint16), ctx.empty((Mb, Mb), np.float32)
+        ctx.copy_h2d(dAb, mi.synth.bf16_normal((Mb, Mb), 1, 1.0 / np.sqrt(Mb)))
+        ctx.copy_h2d(dBb, mi.synth.bf16_normal((Mb, Mb), 2, 1.0 / np.sqrt(Mb)))
+        ms_b = timed(ctx, timer, lambda: ctx.gemm_bf16_f32(dAb, dBb, dCb, Mb, Mb, Mb), max(5, args.steps // 5), 2)
+        tf = 2.0 * Mb ** 3 / (ms_b * 1e-3) / 1e12
+        extras["gemm_bf16_8192"] = {"ms_per_step": round(ms_b, 4), "tflops": round(tf, 1),
+                                    "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+        for b in (dAb, dBb, dCb):
+            b.free()
+        # config 5: MLP
+        Mm, Km, Fm, Nm = 2048, 4096, 11008, 4096
+        dXm, d1, d2 = ctx.empty((Mm, Km), np.int8), ctx.empty((Km, Fm), np.int8), ctx.empty((Fm, Nm), np.int8)
+        dH, dYm = ctx.empty((Mm, Fm), np.int8), ctx.empty((Mm, Nm), np.int8)
+        ctx.fill_i8(dXm, Mm * Km, 3)
+        ctx.fill_i8(d1, Km * Fm, 5)
+        ctx.fill_i8(d2, Fm * Nm, 6)
+        ms_m = timed(ctx, timer, lambda: ctx.mlp_i8(dXm, d1, d2, dH, dYm, Mm, Km, Fm, Nm, 11, 12),
+                     max(5, args.steps // 2), 2)
+        mops = 2.0 * 2 * Mm * Km * Fm
+        extras["mlp_i8"] = {"ms_per_step": round(ms_m, 4), "tops": round(mops / (ms_m * 1e-3) / 1e12, 1),
+                            "frac_of_peak": round(mops / (ms_m * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+        for b in (dXm, d1, d2, dH, dYm):
+            b.free()
+
+    line = {
+        "metric": "int8 GEMM TOPS (% MFMA peak) at 4096^3; int8 conv2d 3x3 GOPS; vs host CPU",
+        "value": round(tops, 2),
+        "unit": "TOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (SplitMix64-seeded int8, generated on the device)",
+        "config": {"workload": "int8 GEMM + requant, M=N=K=4096, A and B row-major (NN), int32 accumulate, "
+                               "Y = sat_int8((acc + 2^9) >> 10)", "M": M, "N": N, "K": K, "shift": 10},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_i8_tile256<NN, Y>",
+            "achieved": round(tops, 2),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TOP/s",
+            "frac": round(tops / PEAK_INT8_TOPS, 4),
+            "traffic": traffic,
+            "alg_bytes_per_launch": M * K + K * N + M * N,
+        },
+        "extras": extras,
+    }
+    ctx.close()
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
