@@ -1,0 +1,65 @@
+"""CPU checks of the C-ABI boundary: the gfx950 library loads on a host
+without a GPU and exports exactly the entry points include/miaie.h declares.
+No compute entry point is called here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import aiehlc_amd as mi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _exported(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_header_declares_the_boundary():
+    names = mi.header_functions()
+    assert len(names) == len(set(names))
+    for must in ("miaie_init", "miaie_finish", "miaie_alloc", "miaie_copy_h2d", "miaie_copy_d2h", "miaie_wait",
+                 "miaie_mm_window_i32", "miaie_gemm_i8_i32", "miaie_gemm_i8_rq", "miaie_gemm_bf16_f32",
+                 "miaie_conv2d_i8_nhwc", "miaie_mlp_i8"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = mi.load_library()
+    declared = set(mi.header_functions())
+    for name in declared:
+        assert hasattr(lib, name), name
+    exported = {s for s in _exported(mi.LIB_PATH) if s.startswith("miaie_")}
+    # hidden visibility: nothing beyond the header leaks out of the library
+    assert exported == declared, (exported ^ declared)
+    # the Python binding table covers the whole header
+    assert set(mi._SIGS) == declared
+
+
+def test_version_and_init_error_without_gpu():
+    lib = mi.load_library()
+    assert mi.version().startswith("miaie")
+    h = ctypes.c_void_p()
+    rc = lib.miaie_init(ctypes.byref(h), 0)
+    if rc != mi.MIAIE_OK:  # no device here: a clean error, never a crash
+        assert rc in (mi.MIAIE_EHIP, mi.MIAIE_EINVAL, mi.MIAIE_EUNSUPPORTED)
+        assert lib.miaie_last_error_string(None)
+        assert h.value is None
+    else:
+        assert lib.miaie_finish(h) == mi.MIAIE_OK
+
+
+def test_null_context_is_rejected():
+    lib = mi.load_library()
+    assert lib.miaie_wait(None, 0) == mi.MIAIE_EINVAL
+    assert lib.miaie_gemm_i8_rq(None, None, None, None, 1, 1, 1, 10, 0, None, 0) == mi.MIAIE_EINVAL
+    assert b"NULL" in lib.miaie_last_error_string(None)
+    assert lib.miaie_finish(None) == mi.MIAIE_OK
+
+
+def test_status_codes_match_header():
+    text = open(mi.HEADER_PATH).read()
+    for name in ("MIAIE_OK", "MIAIE_EINVAL", "MIAIE_EHIP", "MIAIE_ETIMEDOUT", "MIAIE_ENOMEM", "MIAIE_EUNSUPPORTED"):
+        m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
+        assert m and int(m.group(1)) == getattr(mi, name), name
