@@ -18,9 +18,14 @@
 // MFMA operand roles are swapped (srcA = B fragment, srcB = A fragment) so
 // that each lane's accumulator holds 4 consecutive output columns of one row:
 // one dword of int8 output or one 16-byte int32 vector per 4 values.
+#include <type_traits>
+
+#include "gfx950_ops.hpp"
 #include "miaie_internal.hpp"
 
 namespace {
+
+namespace dev = miaie::dev;
 
 // ------------------------------------------------------------- epilogue
 // y = sat_int8(floor((acc + 2^(s-1)) / 2^s)) for s in [1, 31], sat_int8(acc)
@@ -46,129 +51,128 @@ __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) &
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + ((chunk ^ swz(row)) << 4); }
 
 // ---------------------------------------------------------- 256x256 tile
-constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int TILE_BYTES = BM * BK;  // per operand per buffer (16 KiB)
+// Workgroup tile 256x256, k-step 64, four LDS stages of 32 KiB (A then B).
+// The stages are the AIE DMA ping-pong generalised to depth 4: tile t+4 is
+// copied global -> LDS (global_load_lds_dwordx4, no register staging) while
+// tile t is multiplied, so each copy has three tiles of MFMA work to land.
+// Each wave owns a 128x128 quarter: 4x4 v_mfma_i32_32x32x32_i8 per 32-wide
+// k-step, fragments double-buffered in registers so the LDS reads of one
+// k-step overlap the MFMAs of the other.  One barrier per tile.
+//
+// LDS layouts (per stage):
+//   A  [256 rows][64 B]: 16-byte chunk c of row r at chunk c ^ swz(r).
+//   B NT: as A.
+//   B NN [64 k-rows][256 B] (row-major, as stored in memory): 16-byte chunk
+//      c of k-row k at chunk c ^ ((k & 7) << 1).  MFMA fragments (16
+//      consecutive k of one column per lane) are read with two
+//      ds_read_b64_tr_b8, which transpose 8x16 byte blocks on the fly; the
+//      XOR spreads the 8 k-rows x 2 column halves of one read over all banks.
+constexpr int BM = 256, BN = 256, BK = 64, STAGES = 4;
+constexpr int TILE_BYTES = BM * BK;          // one operand of one stage (16 KiB)
+constexpr int STAGE_BYTES = 2 * TILE_BYTES;  // 32 KiB
+constexpr int LDS_BYTES = STAGES * STAGE_BYTES;  // 128 KiB
+constexpr int CP_PER_TILE = 8;               // 16-byte LDS copies per thread per tile
 
 template <bool B_NT, bool WRITE_Y, bool WRITE_C>
 __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
     int relu) {
-  __shared__ __attribute__((aligned(16))) int8_t lds[4 * TILE_BYTES];  // [buf][A|B] = 64 KiB
+  __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+  const uint32_t lds0 = dev::lds_addr(lds);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // ---- tile order: each XCD (workgroups are dealt round-robin to the 8
-  // XCDs) gets a contiguous run of logical tiles, and logical tiles walk
-  // groups of 4 tile-rows column by column, so one XCD's run is a compact
-  // block that shares A rows and B columns in its L2.
-  const int TM = M / BM, TN = N / BN, T = TM * TN;
-  int b = blockIdx.x;
-  int logical = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
-  constexpr int GROUP_M = 4;
-  const int group_size = GROUP_M * TN;
-  const int first_m = (logical / group_size) * GROUP_M;
-  const int gm = min(TM - first_m, GROUP_M);
-  const int tm = first_m + (logical % group_size) % gm;
-  const int tn = (logical % group_size) / gm;
+  int tm, tn;
+  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  // ---- global -> register staging
-  // A: thread loads rows tid/4 + 64*i (i < 4), 16-byte chunk tid%4.
-  const int a_row = tid >> 2, a_chunk = tid & 3;
-  const int8_t* a_src = A + (size_t)(m0 + a_row) * lda + a_chunk * 16;
-  const size_t a_step_rows = (size_t)64 * lda;
-  int a_dst[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a_dst[i] = lds_off(a_row + 64 * i, a_chunk);
-
-  // B, NT: same pattern as A.  B, NN: lane g holds columns 4g..4g+3 of
-  // 16 k-rows (wave w: rows 16w..16w+15), transposed into four 16-byte
-  // k-vectors; lane g stores output q to row 4g + ((q + (g>>2)) & 3) so that
-  // one store instruction covers distinct banks.
-  const int8_t* b_src;
-  size_t b_step;
-  int b_dst[4];
-  uint32_t sel01 = 0, sel23 = 0;
+  // ---- LDS copy assignment.  Copy i (< 4) of wave w fills 1 KiB of a stage:
+  // A (and NT B) rows 64i + 16w + lane/4, physical chunk lane%4;
+  // NN B k-rows 16i + 4w + lane/16, physical chunk lane%16.
+  const int a_r = 16 * wave + (lane >> 2);
+  const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 3) ^ swz(a_r));  // swz(a_r + 64i) == swz(a_r)
+  const int8_t* const a_base = A + (size_t)m0 * lda;
+  uint32_t b_voff;
+  const int8_t* b_base;
   if constexpr (B_NT) {
-    b_src = B + (size_t)(n0 + a_row) * ldb + a_chunk * 16;
-    b_step = (size_t)64 * ldb;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) b_dst[i] = lds_off(a_row + 64 * i, a_chunk);
+    b_voff = (uint32_t)a_r * ldb + 16 * ((lane & 3) ^ swz(a_r));
+    b_base = B + (size_t)n0 * ldb;
   } else {
-    b_src = B + (size_t)(wave * 16) * ldb + n0 + 4 * lane;
-    b_step = (size_t)ldb;
-    const int r = (lane >> 2) & 3;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) b_dst[q] = lds_off(4 * lane + ((q + r) & 3), wave);
-    // stage-1 byte selectors, rotated by r columns: t = [x.b(r), y.b(r), x.b(r+1), y.b(r+1)]
-    const uint32_t c0 = r, c1 = (r + 1) & 3, c2 = (r + 2) & 3, c3 = (r + 3) & 3;
-    sel01 = c0 | ((4 + c0) << 8) | (c1 << 16) | ((4 + c1) << 24);
-    sel23 = c2 | ((4 + c2) << 8) | (c3 << 16) | ((4 + c3) << 24);
+    const int b_r = 4 * wave + (lane >> 4);  // (b_r + 16i) & 7 == b_r & 7
+    b_voff = (uint32_t)b_r * ldb + 16 * ((lane & 15) ^ ((b_r & 7) << 1));
+    b_base = B + n0;
   }
 
-  v4i ra[4];
-  v4i rbv[4];      // NT staging
-  uint32_t rb[16]; // NN staging
-
-  auto load_global = [&](int k0) {
+  auto issue = [&](int kt, int stage) {
+    const uint32_t st = lds0 + stage * STAGE_BYTES + 1024 * wave;
+    const int8_t* ab = a_base + (size_t)kt * BK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      ra[i] = *reinterpret_cast<const v4i*>(a_src + i * a_step_rows + k0);
+    for (int i = 0; i < 4; ++i) dev::gload_lds16(ab + (size_t)(64 * i) * lda, a_voff, st + 4096 * i);
     if constexpr (B_NT) {
+      const int8_t* bb = b_base + (size_t)kt * BK;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        rbv[i] = *reinterpret_cast<const v4i*>(b_src + i * b_step + k0);
+        dev::gload_lds16(bb + (size_t)(64 * i) * ldb, b_voff, st + TILE_BYTES + 4096 * i);
     } else {
+      const int8_t* bb = b_base + (size_t)kt * BK * ldb;
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk)
-        rb[kk] = *reinterpret_cast<const uint32_t*>(b_src + (size_t)(k0 + kk) * b_step);
+      for (int i = 0; i < 4; ++i)
+        dev::gload_lds16(bb + (size_t)(16 * i) * ldb, b_voff, st + TILE_BYTES + 4096 * i);
     }
   };
 
-  auto store_lds = [&](int buf) {
-    int8_t* as = lds + buf * 2 * TILE_BYTES;
-    int8_t* bs = as + TILE_BYTES;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(as + a_dst[i]) = ra[i];
-    if constexpr (B_NT) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(bs + b_dst[i]) = rbv[i];
-    } else {
-      uint32_t o[4][4];  // o[q][d]: column (q + r) & 3, k-rows 4d..4d+3
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t x0 = rb[4 * d], x1 = rb[4 * d + 1], x2 = rb[4 * d + 2], x3 = rb[4 * d + 3];
-        const uint32_t t0 = __builtin_amdgcn_perm(x1, x0, sel01);
-        const uint32_t t1 = __builtin_amdgcn_perm(x1, x0, sel23);
-        const uint32_t t2 = __builtin_amdgcn_perm(x3, x2, sel01);
-        const uint32_t t3 = __builtin_amdgcn_perm(x3, x2, sel23);
-        o[0][d] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-        o[1][d] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-        o[2][d] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-        o[3][d] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        v4i v = {(int)o[q][0], (int)o[q][1], (int)o[q][2], (int)o[q][3]};
-        *reinterpret_cast<v4i*>(bs + b_dst[q]) = v;
-      }
-    }
-  };
-
-  // ---- fragment read offsets: rows wm*128 + 32i + lane%32, logical chunk 2ks + lane/32
+  // ---- fragment offsets within a stage.
+  // A fragment (ks, i): row wm*128 + 32i + lane%32, logical chunk 2ks + lane/32.
   const int wm = wave >> 1, wn = wave & 1;
   const int fr = lane & 31, fh = lane >> 5;
-  int a_frag[2][4], b_frag[2][4];
+  int a_fo[2], b_fo[4];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
+  for (int ks = 0; ks < 2; ++ks) a_fo[ks] = (wm * 128 + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+  if constexpr (B_NT) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      a_frag[ks][i] = lds_off(wm * 128 + 32 * i + fr, 2 * ks + fh);
-      b_frag[ks][i] = lds_off(wn * 128 + 32 * i + fr, 2 * ks + fh);
+    for (int ks = 0; ks < 2; ++ks) b_fo[ks] = TILE_BYTES + (wn * 128 + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+  } else {
+    // tr8 read (ks, j, r): lane 16g + 2jj + h supplies k-row 32ks + 16(g>>1) + 8r + jj,
+    // columns wn*128 + 32j + 16(g&1) + 8h .. +8; it receives column
+    // wn*128 + 32j + lane%32, k = 32ks + 16*(lane/32) + 8r + (0..7).
+    const int g = lane >> 4, jj = (lane >> 1) & 7, h = lane & 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      b_fo[j] = TILE_BYTES + (16 * (g >> 1) + jj) * 256 + (((wn * 8 + 2 * j + (g & 1)) ^ (jj << 1)) << 4) + 8 * h;
+  }
+
+  // One k-step's fragments: 4 A fragments, and 4 B fragments (NT: one
+  // ds_read_b128 each; NN: two tr8 halves each).
+  struct Frags {
+    v4i a[4];
+    v4i b[4];            // NT
+    miaie_v2i lo[4], hi[4];  // NN
+  };
+  constexpr int NREAD = B_NT ? 8 : 12;  // LDS read instructions per k-step
+  // q-th LDS read of k-step ks of `stage` into f
+  auto read_one = [&](int stage, int ks, int q, Frags& f) {
+    const int8_t* s = lds + stage * STAGE_BYTES;
+    if (q < 4) {
+      f.a[q] = *reinterpret_cast<const v4i*>(s + a_fo[ks] + 2048 * q);
+    } else if constexpr (B_NT) {
+      f.b[q - 4] = *reinterpret_cast<const v4i*>(s + b_fo[ks] + 2048 * (q - 4));
+    } else {
+      const int j = (q - 4) >> 1;
+      if ((q & 1) == 0)
+        f.lo[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 8192);
+      else
+        f.hi[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 8192 + 2048);
     }
+  };
+  auto bfrag = [&](const Frags& f, int j) -> v4i {
+    if constexpr (B_NT)
+      return f.b[j];
+    else
+      return v4i{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
+  };
 
   v16i acc[4][4];
 #pragma unroll
@@ -177,31 +181,77 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
     for (int j = 0; j < 4; ++j) acc[i][j] = v16i{0};
 
   const int KT = K / BK;
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
+  // ---- prologue: tiles 0..3 in flight, wait for tile 0
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+    if (s < KT) issue(s, s);
+  if (KT >= 4)
+    dev::wait_vmcnt<3 * CP_PER_TILE>();
+  else if (KT == 3)
+    dev::wait_vmcnt<2 * CP_PER_TILE>();
+  else if (KT == 2)
+    dev::wait_vmcnt<CP_PER_TILE>();
+  else
+    dev::wait_vmcnt<0>();
+  dev::barrier();
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) load_global((kt + 1) * BK);
-    const int8_t* as = lds + cur * 2 * TILE_BYTES;
-    const int8_t* bs = as + TILE_BYTES;
+  Frags f0, f1;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v4i af[4], bf[4];
+  for (int q = 0; q < NREAD; ++q) read_one(0, 0, q, f0);
+
+  // Per tile: phase 1 multiplies k-step 0 (f0) while the reads of k-step 1
+  // (f1) go out between the MFMAs; then the tile barrier; phase 2 multiplies
+  // k-step 1 while the copies of tile kt+4 and the k-step-0 reads of tile
+  // kt+1 go out between the MFMAs.  sched_fence() pins this interleave.
+  // MORE: tile kt+4 exists; NEXT: tile kt+1 exists; VM: copies still allowed
+  // in flight once tile kt+1 has landed.
+  auto tile = [&](int kt, auto more_c, auto next_c, auto vm_c) {
+    constexpr bool MORE = decltype(more_c)::value, NEXT = decltype(next_c)::value;
+    constexpr int VM = decltype(vm_c)::value;
+    const int cur = kt & (STAGES - 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const v4i*>(as + a_frag[ks][i]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const v4i*>(bs + b_frag[ks][j]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+    for (int x = 0; x < 16; ++x) {
+      const int i = x >> 2, j = x & 3;
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
+      if (x < NREAD) read_one(cur, 1, x, f1);
+      dev::sched_fence();
     }
-    if (kt + 1 < KT) store_lds(cur ^ 1);
-    __syncthreads();
-  }
+    // Tile kt+1 must have landed (own copies, then everyone's via the
+    // barrier); after the barrier no wave reads stage `cur` again, so the
+    // copy of tile kt+4 may overwrite it.
+    dev::waitcnt<VM, 0>();
+    dev::barrier();
+    const int nxt = (kt + 1) & (STAGES - 1);
+    const uint32_t st = lds0 + cur * STAGE_BYTES + 1024 * wave;
+    const int8_t* ab = a_base + (size_t)(kt + STAGES) * BK;
+    const int8_t* bb = B_NT ? b_base + (size_t)(kt + STAGES) * BK : b_base + (size_t)(kt + STAGES) * BK * ldb;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int i = x >> 2, j = x & 3;
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
+      if constexpr (MORE) {
+        if (x < 4)
+          dev::gload_lds16(ab + (size_t)(64 * x) * lda, a_voff, st + 4096 * x);
+        else if (x < 8)
+          dev::gload_lds16(bb + (size_t)((B_NT ? 64 : 16) * (x - 4)) * ldb, b_voff, st + TILE_BYTES + 4096 * (x - 4));
+      }
+      if constexpr (NEXT) {
+        if (x < NREAD) read_one(nxt, 0, x, f0);
+      }
+      dev::sched_fence();
+    }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using V2 = std::integral_constant<int, 2 * CP_PER_TILE>;
+  using V1 = std::integral_constant<int, CP_PER_TILE>;
+  using V0 = std::integral_constant<int, 0>;
+  int kt = 0;
+  for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, V2{});
+  if (kt == KT - 4) tile(kt++, F_{}, T_{}, V2{});
+  if (kt == KT - 3) tile(kt++, F_{}, T_{}, V1{});
+  if (kt == KT - 2) tile(kt++, F_{}, T_{}, V0{});
+  tile(kt, F_{}, F_{}, V0{});
 
   // ---- epilogue.  acc[i][j][4g + t]: row m = wm*128 + 32i + lane%32,
   // column n = wn*128 + 32j + 8g + 4*(lane/32) + t.
@@ -220,7 +270,9 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
   }
   if constexpr (WRITE_Y) {
     // Stage the 256x256 int8 tile in LDS (16-byte chunk index XOR row%16),
-    // then write it out with fully coalesced 16-byte stores.
+    // then write it out with fully coalesced 16-byte stores.  Every LDS read
+    // and copy of the main loop completed before its last barrier.
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -354,10 +406,11 @@ namespace miaie {
 // Chooses the kernel.  Y and/or C may be NULL (not both).
 int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
                    int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu) {
+  // The 256x256 kernel copies 16-byte chunks (16-byte aligned operands and
+  // strides) and keeps per-lane offsets of up to 64 rows in 32 bits.
   const bool big = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && aligned(A, 16) &&
-                   aligned(B, 16) && lda % 16 == 0 && (b_nt ? ldb % 16 == 0 : ldb % 4 == 0) &&
-                   (!Y || (aligned(Y, 16) && ldy % 16 == 0)) && (!C || (aligned(C, 16) && ldc % 4 == 0)) &&
-                   (size_t)M * lda < ((size_t)1 << 40);
+                   aligned(B, 16) && lda % 16 == 0 && ldb % 16 == 0 && lda < (1 << 25) && ldb < (1 << 25) &&
+                   (!Y || (aligned(Y, 16) && ldy % 16 == 0)) && (!C || (aligned(C, 16) && ldc % 4 == 0));
   if (big) {
     if (b_nt)
       launch_tile256<true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);

@@ -1,0 +1,90 @@
+// gfx950 device helpers shared by the MFMA kernels: LDS DMA, explicit
+// waits and barriers, LDS transpose reads, and the XCD-aware tile order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#define MIAIE_LDS __attribute__((address_space(3)))
+
+typedef int miaie_v2i __attribute__((ext_vector_type(2)));
+
+namespace miaie {
+namespace dev {
+
+// LDS byte address of a pointer into a __shared__ array (the value M0 and
+// the ds_* instructions take).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const MIAIE_LDS void*)p;
+}
+
+// 16-byte global -> LDS copy (global_load_lds_dwordx4, saddr form): lane l
+// reads 16 bytes at sbase + voff and the wave's 64 x 16 bytes land
+// contiguously at LDS address m0 + 16*l.  Written as inline asm so that the
+// compiler's wait insertion does not treat every later LDS read as aliasing
+// the copy (it would put a vmcnt(0) in front of each); callers therefore
+// wait for their own copies with wait_vmcnt<N>() before the barrier that
+// publishes them.  m0 must be wave-uniform.
+__device__ __forceinline__ void gload_lds16(const void* sbase, uint32_t voff, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+
+// s_waitcnt through the builtin, so that the compiler's own wait insertion
+// sees it (and keeps it: waits written by the program are never dropped).
+// gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14].
+template <int VM, int LGKM>
+__device__ __forceinline__ void waitcnt() {
+  static_assert(VM >= 0 && VM <= 63 && LGKM >= 0 && LGKM <= 15, "waitcnt range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (LGKM << 8));
+}
+// Wait until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() { waitcnt<N, 15>(); }
+__device__ __forceinline__ void wait_lgkmcnt0() { waitcnt<63, 0>(); }
+
+// Workgroup barrier with no implied memory waits (callers wait explicitly).
+// The empty asm statements keep the compiler from moving memory accesses
+// across it.
+__device__ __forceinline__ void barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Keep the scheduler from moving instructions across this point.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// ds_read_b64_tr_b8.  Within each 16-lane group, lane s supplies the address
+// of 8 bytes C_s; lane i receives byte (i & 7) of C_{2j + (i >> 3)} as its
+// byte j (j < 8).  So if lanes 2j and 2j+1 point at bytes [0, 8) and [8, 16)
+// of row j of a row-major byte matrix, lane i receives column i of rows 0..7.
+__device__ __forceinline__ miaie_v2i lds_read_tr8(const void* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((MIAIE_LDS miaie_v2i*)(p));
+}
+
+// ds_read_b64_tr_b16: the 16-bit analogue; lane i receives element (i & 3)
+// of C_{4j + (i >> 2)} as its element j (j < 4), i.e. column i of four
+// 16-element rows supplied by lanes 4j .. 4j+3.
+typedef short miaie_v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ miaie_v4s lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((MIAIE_LDS miaie_v4s*)(p));
+}
+
+// Tile order.  Workgroups are dealt round-robin to the 8 XCDs, so workgroup
+// b runs on XCD b % 8.  Give each XCD a contiguous run of logical tiles, and
+// walk logical tiles in groups of GROUP_M tile-rows, column by column, so one
+// XCD's run is a compact block of tiles sharing A rows and B columns in its L2.
+template <int GROUP_M>
+__device__ __forceinline__ void tile_coords(int b, int TM, int TN, int& tm, int& tn) {
+  const int T = TM * TN;
+  const int logical = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+  const int group_size = GROUP_M * TN;
+  const int first_m = (logical / group_size) * GROUP_M;
+  const int gm = min(TM - first_m, GROUP_M);
+  tm = first_m + (logical % group_size) % gm;
+  tn = (logical % group_size) / gm;
+}
+
+}  // namespace dev
+}  // namespace miaie

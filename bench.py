@@ -120,6 +120,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extras", action="store_true", help="headline workload only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run miaie_copy_d2d of MIB MiB, --steps times (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -130,6 +132,15 @@ def main() -> int:
 
     ctx = mi.Context(0)
     timer = HipTimer(ctx.stream)
+    if args.calibrate_copy:
+        nb = args.calibrate_copy << 20
+        src, dst = ctx.alloc(nb), ctx.alloc(nb)
+        ctx.fill_i8(src, nb, 9)
+        ms = timed(ctx, timer, lambda: ctx.copy_d2d(dst, src, nb), args.steps, args.warmup)
+        print(json.dumps({"calibrate_copy_bytes": nb, "ms_per_copy": round(ms, 5),
+                          "GBps_read_plus_write": round(2 * nb / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        ctx.close()
+        return 0
     M = N = K = 4096
     dA, dB, dY = ctx.empty((M, K), np.int8), ctx.empty((K, N), np.int8), ctx.empty((M, N), np.int8)
     ctx.fill_i8(dA, M * K, 1)
