@@ -37,10 +37,24 @@ __device__ __forceinline__ int requant1(int acc, int s, int relu) {
   return min(max(q, -128), 127);
 }
 
-__device__ __forceinline__ uint32_t requant4(int a0, int a1, int a2, int a3, int s, int relu) {
-  return (uint32_t)(requant1(a0, s, relu) & 0xFF) | ((uint32_t)(requant1(a1, s, relu) & 0xFF) << 8) |
-         ((uint32_t)(requant1(a2, s, relu) & 0xFF) << 16) | ((uint32_t)(requant1(a3, s, relu) & 0xFF) << 24);
-}
+// The same requant in three instructions (add, arithmetic shift, med3) for
+// accumulators with |acc| + 2^(s-1) < 2^31, which holds for any int8 GEMM
+// with K < 2^16 (|acc| <= K * 2^14).  rnd = s ? 2^(s-1) : 0; lo = relu ? 0 : -128
+// (ReLU after the shift is the same as raising the lower clamp to 0).
+struct Requant {
+  int s, rnd, lo, hi;  // hi == 127, kept in a register (VOP3 takes no literal)
+  __device__ __forceinline__ int operator()(int acc) const {
+    int r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"((acc + rnd) >> s), "s"(lo), "v"(hi));
+    return r;
+  }
+  // four results packed little-endian into one dword (byte k = value k)
+  __device__ __forceinline__ uint32_t pack4(int a0, int a1, int a2, int a3) const {
+    const uint32_t lo2 = __builtin_amdgcn_perm((uint32_t)(*this)(a1), (uint32_t)(*this)(a0), 0x0c0c0400u);
+    const uint32_t hi2 = __builtin_amdgcn_perm((uint32_t)(*this)(a3), (uint32_t)(*this)(a2), 0x04000c0cu);
+    return lo2 | hi2;
+  }
+};
 
 // LDS tile rows are 64 bytes = four 16-byte chunks.  The chunk index is
 // XOR-swizzled with bits of the row so that (a) 16 or 8 consecutive rows
@@ -272,6 +286,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
     // Stage the 256x256 int8 tile in LDS (16-byte chunk index XOR row%16),
     // then write it out with fully coalesced 16-byte stores.  Every LDS read
     // and copy of the main loop completed before its last barrier.
+    const Requant rq{shift, shift ? 1 << (shift - 1) : 0, relu ? 0 : -128, 127};
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -281,8 +296,8 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
         for (int g = 0; g < 4; ++g) {
           const int m = wm * 128 + 32 * i + fr;
           const int n = wn * 128 + 32 * j + 8 * g + 4 * fh;
-          const uint32_t packed = requant4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                           acc[i][j][4 * g + 3], shift, relu);
+          const uint32_t packed = rq.pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                           acc[i][j][4 * g + 3]);
           const int off = m * 256 + ((((n >> 4) ^ (m & 15))) << 4) + (n & 15);
           *reinterpret_cast<uint32_t*>(lds + off) = packed;
         }
@@ -407,8 +422,9 @@ namespace miaie {
 int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
                    int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu) {
   // The 256x256 kernel copies 16-byte chunks (16-byte aligned operands and
-  // strides) and keeps per-lane offsets of up to 64 rows in 32 bits.
-  const bool big = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && aligned(A, 16) &&
+  // strides), keeps per-lane offsets of up to 64 rows in 32 bits, and its
+  // requant shortcut needs K < 2^16.
+  const bool big = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && (!Y || K < (1 << 16)) && aligned(A, 16) &&
                    aligned(B, 16) && lda % 16 == 0 && ldb % 16 == 0 && lda < (1 << 25) && ldb < (1 << 25) &&
                    (!Y || (aligned(Y, 16) && ldy % 16 == 0)) && (!C || (aligned(C, 16) && ldc % 4 == 0));
   if (big) {
