@@ -9,98 +9,111 @@
 // the row-major B operand is 16-bit-transposed in registers on its way to LDS.
 //   gemm_bf16_tile256  256x256x32, 4 waves x (4x4 MFMA 32x32x16), LDS double buffer.
 //   gemm_bf16_tile64   64x64x32 bounds-checked fallback.
+#include <type_traits>
+
+#include "gfx950_ops.hpp"
 #include "miaie_internal.hpp"
 
 namespace {
+
+namespace dev = miaie::dev;
 
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + ((chunk ^ swz(row)) << 4); }
 
 __device__ __forceinline__ v8bf as_bf(v4i x) { return __builtin_bit_cast(v8bf, x); }
 
-constexpr int BM = 256, BN = 256, BK = 32;
-constexpr int TILE_BYTES = BM * BK * 2;  // 16 KiB per operand per buffer
+// 256x256 workgroup tile, k-step 32, four 32 KiB LDS stages fed by
+// global_load_lds_dwordx4 (the AIE ping-pong generalised to depth 4), one
+// barrier per tile; each wave owns a 128x128 quarter (4x4
+// v_mfma_f32_32x32x16_bf16 per 16-wide k-step) with register-double-buffered
+// fragments.  Same schedule as the int8 kernel.
+//
+// LDS layouts (per stage):
+//   A  [256 rows][32 bf16 = 64 B]: 16-byte chunk c of row r at c ^ swz(r).
+//   B  [32 k-rows][256 bf16 = 512 B] (row-major as in memory): 16-byte chunk
+//      c of k-row k at c ^ ((k & 3) << 2).  Fragments (8 consecutive k of
+//      one column per lane) come from two ds_read_b64_tr_b16, each
+//      transposing a 4 x 16 block; the XOR puts the 4 k-rows x 64 bytes that
+//      one 32-lane half reads on distinct banks.
+constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4;
+constexpr int TILE_BYTES = BM * BK * 2;       // 16 KiB per operand per stage
+constexpr int STAGE_BYTES = 2 * TILE_BYTES;   // 32 KiB
+constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+constexpr int CP_PER_TILE = 8;                // 16-byte LDS copies per thread per tile
 
 __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __restrict__ A,
                                                             const uint16_t* __restrict__ B,
                                                             float* __restrict__ C, int M, int N, int K) {
-  __shared__ __attribute__((aligned(16))) int8_t lds[4 * TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+  const uint32_t lds0 = dev::lds_addr(lds);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const int TM = M / BM, TN = N / BN, T = TM * TN;
-  const int b = blockIdx.x;
-  const int logical = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
-  constexpr int GROUP_M = 4;
-  const int group_size = GROUP_M * TN;
-  const int first_m = (logical / group_size) * GROUP_M;
-  const int gm = min(TM - first_m, GROUP_M);
-  const int tm = first_m + (logical % group_size) % gm;
-  const int tn = (logical % group_size) / gm;
+  int tm, tn;
+  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  const size_t lda = (size_t)K * 2, ldb = (size_t)N * 2;  // row pitches in bytes
 
-  // A: rows tid/4 + 64i, 16-byte chunk tid%4 (8 bf16 of k)
-  const int a_row = tid >> 2, a_chunk = tid & 3;
-  const uint16_t* a_src = A + (size_t)(m0 + a_row) * K + a_chunk * 8;
-  int a_dst[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a_dst[i] = lds_off(a_row + 64 * i, a_chunk);
+  // Copy i (< 4) of wave w fills 1 KiB of a stage: A rows 64i + 16w + lane/4
+  // (physical chunk lane%4); B k-rows 8i + 2w + lane/32 (physical chunk lane%32).
+  const int a_r = 16 * wave + (lane >> 2);
+  const uint32_t a_voff = (uint32_t)(a_r * lda) + 16 * ((lane & 3) ^ swz(a_r));
+  const int8_t* const a_base = reinterpret_cast<const int8_t*>(A) + (size_t)m0 * lda;
+  const int b_r = 2 * wave + (lane >> 5);  // (b_r + 8i) & 3 == b_r & 3
+  const uint32_t b_voff = (uint32_t)(b_r * ldb) + 16 * ((lane & 31) ^ ((b_r & 3) << 2));
+  const int8_t* const b_base = reinterpret_cast<const int8_t*>(B) + (size_t)n0 * 2;
 
-  // B (K x N): lane g of wave w holds columns n = 2p, 2p+1 with
-  // p = g + 64*(w&1), for k-blocks kb = 2*(w>>1) + u (u < 2), 8 rows each.
-  // Output q goes to row 2p + ((q + f) & 1), f = ((g>>2) ^ (g>>3)) & 1, which
-  // spreads one store instruction over distinct banks.
-  const int p = lane + 64 * (wave & 1);
-  const int kb0 = 2 * (wave >> 1);
-  const uint16_t* b_src = B + (size_t)(kb0 * 8) * N + n0 + 2 * p;
-  const int f = ((lane >> 2) ^ (lane >> 3)) & 1;
-  const uint32_t sel_q0 = f ? 0x07060302u : 0x05040100u;
-  const uint32_t sel_q1 = f ? 0x05040100u : 0x07060302u;
-  int b_dst[2][2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int q = 0; q < 2; ++q) b_dst[u][q] = lds_off(2 * p + ((q + f) & 1), kb0 + u);
-
-  v4i ra[4];
-  uint32_t rb[16];
-
-  auto load_global = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const v4i*>(a_src + (size_t)(64 * i) * K + k0);
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) rb[kk] = *reinterpret_cast<const uint32_t*>(b_src + (size_t)(k0 + kk) * N);
+  auto issue = [&](int kt, int stage, int i) {
+    const uint32_t st = lds0 + stage * STAGE_BYTES + 1024 * wave;
+    if (i < 4)
+      dev::gload_lds16(a_base + (size_t)kt * BK * 2 + (size_t)(64 * i) * lda, a_voff, st + 4096 * i);
+    else
+      dev::gload_lds16(b_base + (size_t)kt * BK * ldb + (size_t)(8 * (i - 4)) * ldb, b_voff,
+                       st + TILE_BYTES + 4096 * (i - 4));
   };
 
-  auto store_lds = [&](int buf) {
-    int8_t* as = lds + buf * 2 * TILE_BYTES;
-    int8_t* bs = as + TILE_BYTES;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(as + a_dst[i]) = ra[i];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      v4i o0, o1;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t x0 = rb[8 * u + 2 * d], x1 = rb[8 * u + 2 * d + 1];
-        o0[d] = (int)__builtin_amdgcn_perm(x1, x0, sel_q0);
-        o1[d] = (int)__builtin_amdgcn_perm(x1, x0, sel_q1);
-      }
-      *reinterpret_cast<v4i*>(bs + b_dst[u][0]) = o0;
-      *reinterpret_cast<v4i*>(bs + b_dst[u][1]) = o1;
-    }
-  };
-
+  // fragment offsets within a stage
   const int wm = wave >> 1, wn = wave & 1;
   const int fr = lane & 31, fh = lane >> 5;
-  int a_frag[2][4], b_frag[2][4];
+  int a_fo[2], b_fo[4];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
+  for (int ks = 0; ks < 2; ++ks) a_fo[ks] = (wm * 128 + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+  {
+    // tr16 read (ks, j, r): lane 16g + 4jj + q supplies k-row 16ks + 8(g>>1) + 4r + jj,
+    // columns wn*128 + 32j + 16(g&1) + 4q .. +4; it receives column
+    // wn*128 + 32j + lane%32 at k = 16ks + 8*(lane/32) + 4r + (0..3).
+    const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      a_frag[ks][i] = lds_off(wm * 128 + 32 * i + fr, 2 * ks + fh);
-      b_frag[ks][i] = lds_off(wn * 128 + 32 * i + fr, 2 * ks + fh);
+    for (int j = 0; j < 4; ++j) {
+      const int c = wn * 16 + 4 * j + 2 * (g & 1) + (q >> 1);
+      b_fo[j] = TILE_BYTES + (8 * (g >> 1) + jj) * 512 + ((c ^ (jj << 2)) << 4) + 8 * (q & 1);
     }
+  }
+
+  struct Frags {
+    v4i a[4];
+    miaie_v4s lo[4], hi[4];
+  };
+  auto read_one = [&](int stage, int ks, int qd, Frags& f) {
+    const int8_t* s = lds + stage * STAGE_BYTES;
+    if (qd < 4) {
+      f.a[qd] = *reinterpret_cast<const v4i*>(s + a_fo[ks] + 2048 * qd);
+    } else {
+      const int j = (qd - 4) >> 1;
+      if ((qd & 1) == 0)
+        f.lo[j] = dev::lds_read_tr16(s + b_fo[j] + ks * 8192);
+      else
+        f.hi[j] = dev::lds_read_tr16(s + b_fo[j] + ks * 8192 + 2048);
+    }
+  };
+  auto bfrag = [&](const Frags& f, int j) -> v8bf {
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s v = {f.lo[j][0], f.lo[j][1], f.lo[j][2], f.lo[j][3], f.hi[j][0], f.hi[j][1], f.hi[j][2], f.hi[j][3]};
+    return __builtin_bit_cast(v8bf, v);
+  };
+  constexpr int NREAD = 12;
 
   v16f acc[4][4];
 #pragma unroll
@@ -109,30 +122,69 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
     for (int j = 0; j < 4; ++j) acc[i][j] = v16f{0.f};
 
   const int KT = K / BK;
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) load_global((kt + 1) * BK);
-    const int8_t* as = lds + cur * 2 * TILE_BYTES;
-    const int8_t* bs = as + TILE_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v4i af[4], bf[4];
+  for (int s = 0; s < STAGES; ++s)
+    if (s < KT) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const v4i*>(as + a_frag[ks][i]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const v4i*>(bs + b_frag[ks][j]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(bf[j]), as_bf(af[i]), acc[i][j], 0, 0, 0);
+      for (int i = 0; i < 8; ++i) issue(s, s, i);
     }
-    if (kt + 1 < KT) store_lds(cur ^ 1);
-    __syncthreads();
-  }
+  if (KT >= 4)
+    dev::wait_vmcnt<3 * CP_PER_TILE>();
+  else if (KT == 3)
+    dev::wait_vmcnt<2 * CP_PER_TILE>();
+  else if (KT == 2)
+    dev::wait_vmcnt<CP_PER_TILE>();
+  else
+    dev::wait_vmcnt<0>();
+  dev::barrier();
+
+  Frags f0, f1;
+#pragma unroll
+  for (int qd = 0; qd < NREAD; ++qd) read_one(0, 0, qd, f0);
+
+  // Phase 1 multiplies k-step 0 while the k-step-1 reads go out; tile
+  // barrier; phase 2 multiplies k-step 1 while the copies of tile kt+4 and
+  // the k-step-0 reads of tile kt+1 go out.
+  auto tile = [&](int kt, auto more_c, auto next_c, auto vm_c) {
+    constexpr bool MORE = decltype(more_c)::value, NEXT = decltype(next_c)::value;
+    constexpr int VM = decltype(vm_c)::value;
+    const int cur = kt & (STAGES - 1);
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int i = x >> 2, j = x & 3;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f0, j), __builtin_bit_cast(v8bf, f0.a[i]),
+                                                          acc[i][j], 0, 0, 0);
+      if (x < NREAD) read_one(cur, 1, x, f1);
+      dev::sched_fence();
+    }
+    dev::waitcnt<VM, 0>();
+    dev::barrier();
+    const int nxt = (kt + 1) & (STAGES - 1);
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int i = x >> 2, j = x & 3;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f1, j), __builtin_bit_cast(v8bf, f1.a[i]),
+                                                          acc[i][j], 0, 0, 0);
+      if constexpr (MORE) {
+        if (x < 8) issue(kt + STAGES, cur, x);
+      }
+      if constexpr (NEXT) {
+        if (x < NREAD) read_one(nxt, 0, x, f0);
+      }
+      dev::sched_fence();
+    }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using V2 = std::integral_constant<int, 2 * CP_PER_TILE>;
+  using V1 = std::integral_constant<int, CP_PER_TILE>;
+  using V0 = std::integral_constant<int, 0>;
+  int kt = 0;
+  for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, V2{});
+  if (kt == KT - 4) tile(kt++, F_{}, T_{}, V2{});
+  if (kt == KT - 3) tile(kt++, F_{}, T_{}, V1{});
+  if (kt == KT - 2) tile(kt++, F_{}, T_{}, V0{});
+  tile(kt, F_{}, F_{}, V0{});
 
   // acc[i][j][4g + t]: row m = wm*128 + 32i + lane%32, column n = wn*128 + 32j + 8g + 4*(lane/32) + t
 #pragma unroll
@@ -205,8 +257,10 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restri
 namespace miaie {
 
 int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float* C, int M, int N, int K) {
-  const bool big = M % BM == 0 && N % BN == 0 && K % BK == 0 && N % 2 == 0 && aligned(A, 16) &&
-                   aligned(B, 16) && aligned(C, 16);
+  // 256x256 kernel: whole tiles, 16-byte aligned operands, per-lane copy
+  // offsets of up to 64 rows in 32 bits.
+  const bool big = M % BM == 0 && N % BN == 0 && K % BK == 0 && aligned(A, 16) && aligned(B, 16) &&
+                   aligned(C, 16) && K < (1 << 24) && N < (1 << 24);
   if (big) {
     hipLaunchKernelGGL(gemm_bf16_tile256, dim3((M / BM) * (N / BN)), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
     return check_launch(ctx, "gemm_bf16_tile256");

@@ -9,6 +9,7 @@
 #define MIAIE_LDS __attribute__((address_space(3)))
 
 typedef int miaie_v2i __attribute__((ext_vector_type(2)));
+typedef short miaie_v4s __attribute__((ext_vector_type(4)));
 
 namespace miaie {
 namespace dev {
@@ -66,7 +67,6 @@ __device__ __forceinline__ miaie_v2i lds_read_tr8(const void* p) {
 // ds_read_b64_tr_b16: the 16-bit analogue; lane i receives element (i & 3)
 // of C_{4j + (i >> 2)} as its element j (j < 4), i.e. column i of four
 // 16-element rows supplied by lanes 4j .. 4j+3.
-typedef short miaie_v4s __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ miaie_v4s lds_read_tr16(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((MIAIE_LDS miaie_v4s*)(p));
 }
