@@ -146,6 +146,137 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
   *reinterpret_cast<uint4*>(Y + (size_t)(p0 + p) * Cout + co0 + c16) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
+// Row-pair kernel for stride-1 convolutions with Wo <= 64 (instantiated for
+// 3x3 filters and Cin in {32, 64}).  A workgroup owns two output rows of one
+// image (64 columns, padded) and one 64-channel block of Cout.  It stages in
+// LDS once, with every global load of the staging in flight together:
+//   X  the R+1 input rows the two output rows touch, with the zero padding
+//      columns and rows materialised, [row][col][Cin bytes], 16-byte chunk
+//      c of column col at c ^ xswz(col) (conflict-free fragment reads);
+//   W  the 64 output channels' OHWI rows, pitch R*S*Cin + 16 bytes.
+// Each of the 8 waves then owns 32 output pixels x 32 channels and runs the
+// whole k = (r, s, ci) reduction from LDS (one v_mfma_i32_32x32x32_i8 per
+// 32-wide k-step, fully unrolled), so there is no im2col buffer and no
+// cross-wave reduction.  The int8 results are staged in LDS and leave as
+// contiguous NHWC rows.
+constexpr int ROWS = 2;   // output rows per workgroup
+constexpr int PB = 64;    // output columns per row (padded)
+constexpr int RCOB = 64;  // output channels per workgroup
+
+template <int CIN>
+__device__ __forceinline__ int xswz(int col) {
+  return (col * CIN / 256) & (CIN / 16 - 1);
+}
+
+template <int R, int S, int CIN>
+struct RowsGeom {
+  static constexpr int XR = ROWS + R - 1, XC = PB + S - 1;  // staged input rows / columns
+  static constexpr int NCH = CIN / 16;                      // 16-byte chunks per pixel
+  static constexpr int XTOT = XR * XC * NCH;                // X chunks
+  static constexpr int RSC = R * S * CIN, WP = RSC + 16;    // weight row length / LDS pitch
+  static constexpr int WTOT = RCOB * RSC / 16;              // W chunks
+  static constexpr int XQ = (XTOT + 511) / 512, WQ = (WTOT + 511) / 512;
+  static constexpr int X_BYTES = XR * XC * CIN;
+  static constexpr int LDS = X_BYTES + RCOB * WP;
+  static constexpr int T = R * S * CIN / 32;                // 32-wide k-steps
+  static_assert(LDS <= 65536 && ROWS * PB * RCOB <= LDS, "row-pair conv LDS budget");
+};
+
+template <int R, int S, int CIN>
+__global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
+                                                      const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
+                                                      int H, int Wd, int Cout, int pad, int Ho, int Wo) {
+  using G = RowsGeom<R, S, CIN>;
+  __shared__ __attribute__((aligned(16))) int8_t smem[G::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int rows_per_img = (Ho + ROWS - 1) / ROWS;
+  const int n = blockIdx.x / rows_per_img;
+  const int ho0 = (blockIdx.x % rows_per_img) * ROWS;
+  const int co0 = blockIdx.y * RCOB;
+  int8_t* const xs = smem;
+  int8_t* const ws = smem + G::X_BYTES;
+
+  // ---- stage X (zero outside the image) and W: all loads first, then the LDS writes
+  v4i xv[G::XQ], wv[G::WQ];
+#pragma unroll
+  for (int u = 0; u < G::XQ; ++u) {
+    const int q = tid + 512 * u;
+    const int c = q % G::NCH, rc = q / G::NCH;
+    const int col = rc % G::XC, row = rc / G::XC;
+    const int hi = ho0 + row - pad, wi = col - pad;
+    xv[u] = v4i{0};
+    if (q < G::XTOT && hi >= 0 && hi < H && wi >= 0 && wi < Wd)
+      xv[u] = *reinterpret_cast<const v4i*>(X + (((size_t)n * H + hi) * Wd + wi) * CIN + 16 * c);
+  }
+#pragma unroll
+  for (int u = 0; u < G::WQ; ++u) {
+    const int q = tid + 512 * u;
+    if (q < G::WTOT)
+      wv[u] = *reinterpret_cast<const v4i*>(W + (size_t)co0 * G::RSC + 16 * (size_t)q);
+  }
+#pragma unroll
+  for (int u = 0; u < G::XQ; ++u) {
+    const int q = tid + 512 * u;
+    const int c = q % G::NCH, rc = q / G::NCH;
+    const int col = rc % G::XC, row = rc / G::XC;
+    if (q < G::XTOT) *reinterpret_cast<v4i*>(xs + (row * G::XC + col) * CIN + ((c ^ xswz<CIN>(col)) << 4)) = xv[u];
+  }
+#pragma unroll
+  for (int u = 0; u < G::WQ; ++u) {
+    const int q = tid + 512 * u;
+    const int c = q % (G::RSC / 16), row = q / (G::RSC / 16);
+    if (q < G::WTOT) *reinterpret_cast<v4i*>(ws + row * G::WP + 16 * c) = wv[u];
+  }
+  __syncthreads();
+
+  // ---- wave: output row rr, pixels 32pb .. +32, channels 32wc .. +32
+  const int rr = wave >> 2, pb = (wave >> 1) & 1, wc = wave & 1;
+  const int px = 32 * pb + fr;
+  const int8_t* wrow = ws + (32 * wc + fr) * G::WP + 16 * fh;
+  v16i acc = v16i{0};
+#pragma unroll
+  for (int t = 0; t < G::T; ++t) {
+    const int cib = t % (CIN / 32), rs = t / (CIN / 32);
+    const int r = rs / S, s = rs % S;
+    const int col = px + s;
+    const v4i xf = *reinterpret_cast<const v4i*>(xs + ((rr + r) * G::XC + col) * CIN +
+                                                 (((2 * cib + fh) ^ xswz<CIN>(col)) << 4));
+    const v4i wf = *reinterpret_cast<const v4i*>(wrow + 32 * t);
+    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, xf, acc, 0, 0, 0);
+  }
+
+  // ---- requant (per channel) and stage [row][px][64 ch] in LDS.
+  // acc[4g + tt]: channel 32wc + 8g + 4*(lane/32) + tt, pixel px.
+  uint32_t sh4[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) sh4[g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc + 8 * g + 4 * fh);
+  __syncthreads();  // all fragment reads done before the staging overwrites X
+  int8_t* const os = smem;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int cc = 32 * wc + 8 * g + 4 * fh;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+      packed |= (uint32_t)(requant1(acc[4 * g + tt], (sh4[g] >> (8 * tt)) & 0xFF) & 0xFF) << (8 * tt);
+    const int off = (rr * PB + px) * RCOB + ((((cc >> 4) ^ ((px >> 2) & 3))) << 4) + (cc & 15);
+    *reinterpret_cast<uint32_t*>(os + off) = packed;
+  }
+  __syncthreads();
+  // ---- copy out: (row, pixel, 16-byte chunk) per thread
+#pragma unroll
+  for (int u = 0; u < ROWS * PB * 4 / 512; ++u) {
+    const int q = tid + 512 * u;
+    const int c = q & 3, p = (q >> 2) % PB, row = q / (4 * PB);
+    const int ho = ho0 + row;
+    if (ho < Ho && p < Wo) {
+      const v4i v = *reinterpret_cast<const v4i*>(os + (row * PB + p) * RCOB + ((c ^ ((p >> 2) & 3)) << 4));
+      *reinterpret_cast<v4i*>(Y + (((size_t)n * Ho + ho) * Wo + p) * Cout + co0 + 16 * c) = v;
+    }
+  }
+}
+
 // Any-shape fallback: one thread per output element.
 __global__ __launch_bounds__(256) void conv2d_i8_direct(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
                                                         const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
@@ -184,6 +315,20 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
   const int Ho = (H + 2 * pad - R) / stride + 1;
   const int Wo = (Wd + 2 * pad - S) / stride + 1;
   const size_t P = (size_t)N * Ho * Wo;
+  // Row-pair kernel (3x3, stride 1, Cin 32 or 64, Wo <= 64).
+  const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64) && Cout % RCOB == 0 &&
+                       Wo <= PB && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) && aligned(shifts, 4) &&
+                       (size_t)N * ((Ho + ROWS - 1) / ROWS) < ((size_t)1 << 31);
+  if (rows_ok) {
+    dim3 grid((unsigned)(N * ((Ho + ROWS - 1) / ROWS)), Cout / RCOB);
+    if (Cin == 64)
+      hipLaunchKernelGGL((conv2d_i8_rows<3, 3, 64>), grid, dim3(512), 0, ctx->stream, X, W, shifts, Y, H, Wd, Cout,
+                         pad, Ho, Wo);
+    else
+      hipLaunchKernelGGL((conv2d_i8_rows<3, 3, 32>), grid, dim3(512), 0, ctx->stream, X, W, shifts, Y, H, Wd, Cout,
+                         pad, Ho, Wo);
+    return check_launch(ctx, "conv2d_i8_rows");
+  }
   const bool fast = Cin % 32 == 0 && Cout % COB == 0 && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) &&
                     P < ((size_t)1 << 31) && (P + PIX - 1) / PIX < ((size_t)1 << 31);
   if (fast) {

@@ -158,6 +158,9 @@ CONV_SHAPES = [
     (1, 8, 8, 64, 128, 3, 3, 2, 1),
     (1, 6, 6, 96, 64, 1, 1, 1, 0),
     (1, 9, 9, 32, 64, 5, 5, 1, 2),
+    (1, 7, 64, 64, 128, 3, 3, 1, 1),  # odd Ho, Wo = 64, two Cout blocks
+    (3, 5, 33, 32, 64, 3, 3, 1, 0),   # no padding
+    (2, 56, 56, 64, 64, 3, 3, 1, 1),  # config shape, fewer images
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # fallback kernel (channels not multiples of 32/64)
     (2, 6, 7, 3, 5, 3, 3, 2, 0),      # fallback kernel
 ]
