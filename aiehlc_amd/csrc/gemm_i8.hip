@@ -64,35 +64,52 @@ struct Requant {
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + ((chunk ^ swz(row)) << 4); }
 
-// ---------------------------------------------------------- 256x256 tile
-// Workgroup tile 256x256, k-step 64, four LDS stages of 32 KiB (A then B).
+// ---------------------------------------------------------- pipelined tile
+// Workgroup tile 256 x BN (BN = 256 or 128), k-step 64, four LDS stages.
 // The stages are the AIE DMA ping-pong generalised to depth 4: tile t+4 is
 // copied global -> LDS (global_load_lds_dwordx4, no register staging) while
 // tile t is multiplied, so each copy has three tiles of MFMA work to land.
-// Each wave owns a 128x128 quarter: 4x4 v_mfma_i32_32x32x32_i8 per 32-wide
-// k-step, fragments double-buffered in registers so the LDS reads of one
-// k-step overlap the MFMAs of the other.  One barrier per tile.
+// Each of the 4 waves owns a 128 x BN/2 quarter: 4 x (BN/64)
+// v_mfma_i32_32x32x32_i8 per 32-wide k-step, fragments double-buffered in
+// registers so the LDS reads of one k-step overlap the MFMAs of the other.
+// One barrier per tile.  BN = 128 halves the work per tile, for shapes whose
+// 256-wide tiles would leave CUs idle.
 //
 // LDS layouts (per stage):
 //   A  [256 rows][64 B]: 16-byte chunk c of row r at chunk c ^ swz(r).
-//   B NT: as A.
-//   B NN [64 k-rows][256 B] (row-major, as stored in memory): 16-byte chunk
-//      c of k-row k at chunk c ^ ((k & 7) << 1).  MFMA fragments (16
-//      consecutive k of one column per lane) are read with two
-//      ds_read_b64_tr_b8, which transpose 8x16 byte blocks on the fly; the
-//      XOR spreads the 8 k-rows x 2 column halves of one read over all banks.
-constexpr int BM = 256, BN = 256, BK = 64, STAGES = 4;
-constexpr int TILE_BYTES = BM * BK;          // one operand of one stage (16 KiB)
-constexpr int STAGE_BYTES = 2 * TILE_BYTES;  // 32 KiB
-constexpr int LDS_BYTES = STAGES * STAGE_BYTES;  // 128 KiB
-constexpr int CP_PER_TILE = 8;               // 16-byte LDS copies per thread per tile
+//   B NT [BN rows][64 B]: as A.
+//   B NN [64 k-rows][BN B] (row-major, as stored in memory): 16-byte chunk
+//      c of k-row k at chunk c ^ bswz(k).  MFMA fragments (16 consecutive k
+//      of one column per lane) are read with two ds_read_b64_tr_b8, which
+//      transpose 8x16 byte blocks on the fly; bswz spreads the 8 k-rows x 2
+//      column halves one 32-lane half reads over all banks.
+constexpr int BM = 256, BK = 64, STAGES = 4;
 
-template <bool B_NT, bool WRITE_Y, bool WRITE_C>
-__global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
+template <int BN>
+struct PipeGeom {
+  static constexpr int A_BYTES = BM * BK;             // 16 KiB
+  static constexpr int B_BYTES = BN * BK;             // 16 or 8 KiB
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+  static constexpr int B_CP = B_BYTES / 4096;          // B copies per thread per tile (4 or 2)
+  static constexpr int CP_PER_TILE = 4 + B_CP;         // 16-byte LDS copies per thread per tile
+  static constexpr int NJ = BN / 64;                   // B fragments per wave per k-step
+  static constexpr int NMF = 4 * NJ;                   // MFMAs per wave per k-step
+  static_assert(BM * BN <= LDS_BYTES, "Y staging fits in the stages");
+};
+
+template <int BN>
+__device__ __forceinline__ int bswz(int k) {
+  return BN == 256 ? (k & 7) << 1 : ((k >> 1) & 3) << 1;
+}
+
+template <int BN, bool B_NT, bool WRITE_Y, bool WRITE_C>
+__global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
     int relu) {
-  __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+  using G = PipeGeom<BN>;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS_BYTES];
   const uint32_t lds0 = dev::lds_addr(lds);
 
   const int tid = threadIdx.x;
@@ -103,38 +120,36 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
   dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  // ---- LDS copy assignment.  Copy i (< 4) of wave w fills 1 KiB of a stage:
-  // A (and NT B) rows 64i + 16w + lane/4, physical chunk lane%4;
-  // NN B k-rows 16i + 4w + lane/16, physical chunk lane%16.
+  // ---- LDS copy assignment.  Copy i of wave w fills the 1 KiB block 4i + w
+  // of an operand's stage region:
+  //   A (and NT B): rows 64i + 16w + lane/4, physical chunk lane%4;
+  //   NN B: k-rows (4i + w) * (1024 / BN) + lane / (BN / 16), physical chunk
+  //   lane % (BN / 16).
   const int a_r = 16 * wave + (lane >> 2);
   const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 3) ^ swz(a_r));  // swz(a_r + 64i) == swz(a_r)
   const int8_t* const a_base = A + (size_t)m0 * lda;
   uint32_t b_voff;
   const int8_t* b_base;
+  constexpr int B_ROWS_PER_CP = B_NT ? 64 : 4096 / BN;  // operand rows between copies i and i+1
   if constexpr (B_NT) {
     b_voff = (uint32_t)a_r * ldb + 16 * ((lane & 3) ^ swz(a_r));
     b_base = B + (size_t)n0 * ldb;
   } else {
-    const int b_r = 4 * wave + (lane >> 4);  // (b_r + 16i) & 7 == b_r & 7
-    b_voff = (uint32_t)b_r * ldb + 16 * ((lane & 15) ^ ((b_r & 7) << 1));
+    constexpr int CPR = BN / 16;  // 16-byte chunks per k-row
+    const int b_r = (1024 / BN) * wave + lane / CPR;  // bswz(b_r + B_ROWS_PER_CP * i) == bswz(b_r)
+    b_voff = (uint32_t)b_r * ldb + 16 * ((lane % CPR) ^ bswz<BN>(b_r));
     b_base = B + n0;
   }
 
-  auto issue = [&](int kt, int stage) {
-    const uint32_t st = lds0 + stage * STAGE_BYTES + 1024 * wave;
-    const int8_t* ab = a_base + (size_t)kt * BK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dev::gload_lds16(ab + (size_t)(64 * i) * lda, a_voff, st + 4096 * i);
-    if constexpr (B_NT) {
-      const int8_t* bb = b_base + (size_t)kt * BK;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dev::gload_lds16(bb + (size_t)(64 * i) * ldb, b_voff, st + TILE_BYTES + 4096 * i);
+  // copy x (< CP_PER_TILE) of tile kt into stage `stage`
+  auto copy = [&](int kt, int stage, int x) {
+    const uint32_t st = lds0 + stage * G::STAGE_BYTES + 1024 * wave;
+    if (x < 4) {
+      dev::gload_lds16(a_base + (size_t)kt * BK + (size_t)(64 * x) * lda, a_voff, st + 4096 * x);
     } else {
-      const int8_t* bb = b_base + (size_t)kt * BK * ldb;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dev::gload_lds16(bb + (size_t)(16 * i) * ldb, b_voff, st + TILE_BYTES + 4096 * i);
+      const int i = x - 4;
+      const int8_t* bb = B_NT ? b_base + (size_t)kt * BK : b_base + (size_t)kt * BK * ldb;
+      dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * i) * ldb, b_voff, st + G::A_BYTES + 4096 * i);
     }
   };
 
@@ -147,28 +162,32 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
   for (int ks = 0; ks < 2; ++ks) a_fo[ks] = (wm * 128 + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
   if constexpr (B_NT) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) b_fo[ks] = TILE_BYTES + (wn * 128 + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+    for (int ks = 0; ks < 2; ++ks)
+      b_fo[ks] = G::A_BYTES + (wn * (BN / 2) + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
   } else {
     // tr8 read (ks, j, r): lane 16g + 2jj + h supplies k-row 32ks + 16(g>>1) + 8r + jj,
-    // columns wn*128 + 32j + 16(g&1) + 8h .. +8; it receives column
-    // wn*128 + 32j + lane%32, k = 32ks + 16*(lane/32) + 8r + (0..7).
+    // columns wn*BN/2 + 32j + 16(g&1) + 8h .. +8; it receives column
+    // wn*BN/2 + 32j + lane%32, k = 32ks + 16*(lane/32) + 8r + (0..7).
+    // bswz of those k-rows depends on jj only.
     const int g = lane >> 4, jj = (lane >> 1) & 7, h = lane & 1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      b_fo[j] = TILE_BYTES + (16 * (g >> 1) + jj) * 256 + (((wn * 8 + 2 * j + (g & 1)) ^ (jj << 1)) << 4) + 8 * h;
+    for (int j = 0; j < G::NJ; ++j) {
+      const int c = wn * (BN / 32) + 2 * j + (g & 1);
+      b_fo[j] = G::A_BYTES + (16 * (g >> 1) + jj) * BN + ((c ^ bswz<BN>(jj)) << 4) + 8 * h;
+    }
   }
 
-  // One k-step's fragments: 4 A fragments, and 4 B fragments (NT: one
+  // One k-step's fragments: 4 A fragments, and NJ B fragments (NT: one
   // ds_read_b128 each; NN: two tr8 halves each).
   struct Frags {
     v4i a[4];
-    v4i b[4];            // NT
-    miaie_v2i lo[4], hi[4];  // NN
+    v4i b[G::NJ];                  // NT
+    miaie_v2i lo[G::NJ], hi[G::NJ];  // NN
   };
-  constexpr int NREAD = B_NT ? 8 : 12;  // LDS read instructions per k-step
+  constexpr int NREAD = 4 + (B_NT ? 1 : 2) * G::NJ;  // LDS read instructions per k-step
   // q-th LDS read of k-step ks of `stage` into f
   auto read_one = [&](int stage, int ks, int q, Frags& f) {
-    const int8_t* s = lds + stage * STAGE_BYTES;
+    const int8_t* s = lds + stage * G::STAGE_BYTES;
     if (q < 4) {
       f.a[q] = *reinterpret_cast<const v4i*>(s + a_fo[ks] + 2048 * q);
     } else if constexpr (B_NT) {
@@ -176,9 +195,9 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
     } else {
       const int j = (q - 4) >> 1;
       if ((q & 1) == 0)
-        f.lo[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 8192);
+        f.lo[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN);
       else
-        f.hi[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 8192 + 2048);
+        f.hi[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN + 8 * BN);
     }
   };
   auto bfrag = [&](const Frags& f, int j) -> v4i {
@@ -188,23 +207,27 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
       return v4i{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
   };
 
-  v16i acc[4][4];
+  v16i acc[4][G::NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v16i{0};
+    for (int j = 0; j < G::NJ; ++j) acc[i][j] = v16i{0};
 
   const int KT = K / BK;
+  constexpr int CP = G::CP_PER_TILE;
   // ---- prologue: tiles 0..3 in flight, wait for tile 0
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
-    if (s < KT) issue(s, s);
+    if (s < KT) {
+#pragma unroll
+      for (int x = 0; x < CP; ++x) copy(s, s, x);
+    }
   if (KT >= 4)
-    dev::wait_vmcnt<3 * CP_PER_TILE>();
+    dev::wait_vmcnt<3 * CP>();
   else if (KT == 3)
-    dev::wait_vmcnt<2 * CP_PER_TILE>();
+    dev::wait_vmcnt<2 * CP>();
   else if (KT == 2)
-    dev::wait_vmcnt<CP_PER_TILE>();
+    dev::wait_vmcnt<CP>();
   else
     dev::wait_vmcnt<0>();
   dev::barrier();
@@ -224,11 +247,15 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
     constexpr int VM = decltype(vm_c)::value;
     const int cur = kt & (STAGES - 1);
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int i = x >> 2, j = x & 3;
+    for (int x = 0; x < G::NMF; ++x) {
+      const int i = x / G::NJ, j = x % G::NJ;
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
       if (x < NREAD) read_one(cur, 1, x, f1);
       dev::sched_fence();
+    }
+    if constexpr (NREAD > G::NMF) {
+#pragma unroll
+      for (int q = G::NMF; q < NREAD; ++q) read_one(cur, 1, q, f1);
     }
     // Tile kt+1 must have landed (own copies, then everyone's via the
     // barrier); after the barrier no wave reads stage `cur` again, so the
@@ -236,29 +263,31 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
     dev::waitcnt<VM, 0>();
     dev::barrier();
     const int nxt = (kt + 1) & (STAGES - 1);
-    const uint32_t st = lds0 + cur * STAGE_BYTES + 1024 * wave;
-    const int8_t* ab = a_base + (size_t)(kt + STAGES) * BK;
-    const int8_t* bb = B_NT ? b_base + (size_t)(kt + STAGES) * BK : b_base + (size_t)(kt + STAGES) * BK * ldb;
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int i = x >> 2, j = x & 3;
+    for (int x = 0; x < G::NMF; ++x) {
+      const int i = x / G::NJ, j = x % G::NJ;
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
       if constexpr (MORE) {
-        if (x < 4)
-          dev::gload_lds16(ab + (size_t)(64 * x) * lda, a_voff, st + 4096 * x);
-        else if (x < 8)
-          dev::gload_lds16(bb + (size_t)((B_NT ? 64 : 16) * (x - 4)) * ldb, b_voff, st + TILE_BYTES + 4096 * (x - 4));
+        if (x < CP) copy(kt + STAGES, cur, x);
       }
       if constexpr (NEXT) {
         if (x < NREAD) read_one(nxt, 0, x, f0);
       }
       dev::sched_fence();
     }
+    if constexpr (MORE && CP > G::NMF) {
+#pragma unroll
+      for (int x = G::NMF; x < CP; ++x) copy(kt + STAGES, cur, x);
+    }
+    if constexpr (NEXT && NREAD > G::NMF) {
+#pragma unroll
+      for (int q = G::NMF; q < NREAD; ++q) read_one(nxt, 0, q, f0);
+    }
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
-  using V2 = std::integral_constant<int, 2 * CP_PER_TILE>;
-  using V1 = std::integral_constant<int, CP_PER_TILE>;
+  using V2 = std::integral_constant<int, 2 * CP>;
+  using V1 = std::integral_constant<int, CP>;
   using V0 = std::integral_constant<int, 0>;
   int kt = 0;
   for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, V2{});
@@ -268,45 +297,47 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_tile256(
   tile(kt, F_{}, F_{}, V0{});
 
   // ---- epilogue.  acc[i][j][4g + t]: row m = wm*128 + 32i + lane%32,
-  // column n = wn*128 + 32j + 8g + 4*(lane/32) + t.
+  // column n = wn*BN/2 + 32j + 8g + 4*(lane/32) + t.
   if constexpr (WRITE_C) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < G::NJ; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int m = m0 + wm * 128 + 32 * i + fr;
-          const int n = n0 + wn * 128 + 32 * j + 8 * g + 4 * fh;
+          const int n = n0 + wn * (BN / 2) + 32 * j + 8 * g + 4 * fh;
           v4i v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
           *reinterpret_cast<v4i*>(C + (size_t)m * ldc + n) = v;
         }
   }
   if constexpr (WRITE_Y) {
-    // Stage the 256x256 int8 tile in LDS (16-byte chunk index XOR row%16),
-    // then write it out with fully coalesced 16-byte stores.  Every LDS read
-    // and copy of the main loop completed before its last barrier.
+    // Stage the 256 x BN int8 tile in LDS (16-byte chunk index XOR row%16,
+    // within the row's BN/16 chunks), then write it out with fully coalesced
+    // 16-byte stores.  Every LDS read and copy of the main loop completed
+    // before its last barrier.
+    constexpr int CH = BN / 16;
     const Requant rq{shift, shift ? 1 << (shift - 1) : 0, relu ? 0 : -128, 127};
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < G::NJ; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int m = wm * 128 + 32 * i + fr;
-          const int n = wn * 128 + 32 * j + 8 * g + 4 * fh;
+          const int n = wn * (BN / 2) + 32 * j + 8 * g + 4 * fh;
           const uint32_t packed = rq.pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                                            acc[i][j][4 * g + 3]);
-          const int off = m * 256 + ((((n >> 4) ^ (m & 15))) << 4) + (n & 15);
+          const int off = m * BN + ((((n >> 4) ^ (m & (CH - 1)))) << 4) + (n & 15);
           *reinterpret_cast<uint32_t*>(lds + off) = packed;
         }
     __syncthreads();
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < BM * CH / 256; ++it) {
       const int flat = it * 256 + tid;
-      const int m = flat >> 4, c = flat & 15;
-      const v4i v = *reinterpret_cast<const v4i*>(lds + m * 256 + ((c ^ (m & 15)) << 4));
+      const int m = flat / CH, c = flat % CH;
+      const v4i v = *reinterpret_cast<const v4i*>(lds + m * BN + ((c ^ (m & (CH - 1))) << 4));
       *reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + c * 16) = v;
     }
   }
@@ -399,19 +430,31 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64(const int8_t* __restrict__
   }
 }
 
-template <bool B_NT>
-void launch_tile256(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
-                    int N, int K, int lda, int ldb, int ldy, int ldc, int shift, int relu) {
+template <int BN, bool B_NT>
+void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
+                 int lda, int ldb, int ldy, int ldc, int shift, int relu) {
   dim3 grid((M / BM) * (N / BN)), block(256);
   if (Y && C)
-    hipLaunchKernelGGL((gemm_i8_tile256<B_NT, true, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda,
-                       ldb, ldy, ldc, shift, relu);
+    hipLaunchKernelGGL((gemm_i8_pipe<BN, B_NT, true, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb,
+                       ldy, ldc, shift, relu);
   else if (Y)
-    hipLaunchKernelGGL((gemm_i8_tile256<B_NT, true, false>), grid, block, 0, st, A, B, Y, C, M, N, K,
-                       lda, ldb, ldy, ldc, shift, relu);
+    hipLaunchKernelGGL((gemm_i8_pipe<BN, B_NT, true, false>), grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb,
+                       ldy, ldc, shift, relu);
   else
-    hipLaunchKernelGGL((gemm_i8_tile256<B_NT, false, true>), grid, block, 0, st, A, B, Y, C, M, N, K,
-                       lda, ldb, ldy, ldc, shift, relu);
+    hipLaunchKernelGGL((gemm_i8_pipe<BN, B_NT, false, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb,
+                       ldy, ldc, shift, relu);
+}
+
+// Tile width for the pipelined kernel: 256 unless 128-wide tiles finish the
+// grid in fewer rounds of 256 workgroups (one per CU), counting a 128-wide
+// tile as 0.55 of a 256-wide one.  0: neither fits the shape.
+int pick_bn(int M, int N) {
+  if (M % BM != 0) return 0;
+  const long rounds256 = N % 256 == 0 ? ((long)(M / BM) * (N / 256) + 255) / 256 : -1;
+  const long rounds128 = N % 128 == 0 ? ((long)(M / BM) * (N / 128) + 255) / 256 : -1;
+  if (rounds256 < 0) return rounds128 < 0 ? 0 : 128;
+  if (rounds128 < 0) return 256;
+  return rounds128 * 55 < rounds256 * 100 ? 128 : 256;
 }
 
 }  // namespace
@@ -424,15 +467,20 @@ int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, 
   // The 256x256 kernel copies 16-byte chunks (16-byte aligned operands and
   // strides), keeps per-lane offsets of up to 64 rows in 32 bits, and its
   // requant shortcut needs K < 2^16.
-  const bool big = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && (!Y || K < (1 << 16)) && aligned(A, 16) &&
+  const int bn = pick_bn(M, N);
+  const bool big = bn != 0 && (K % BK == 0) && (!Y || K < (1 << 16)) && aligned(A, 16) &&
                    aligned(B, 16) && lda % 16 == 0 && ldb % 16 == 0 && lda < (1 << 25) && ldb < (1 << 25) &&
                    (!Y || (aligned(Y, 16) && ldy % 16 == 0)) && (!C || (aligned(C, 16) && ldc % 4 == 0));
   if (big) {
-    if (b_nt)
-      launch_tile256<true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+    if (bn == 256 && b_nt)
+      launch_pipe<256, true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+    else if (bn == 256)
+      launch_pipe<256, false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+    else if (b_nt)
+      launch_pipe<128, true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
     else
-      launch_tile256<false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
-    return check_launch(ctx, "gemm_i8_tile256");
+      launch_pipe<128, false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+    return check_launch(ctx, "gemm_i8_pipe");
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64), block(256);
   if (grid.y > 65535) return fail(ctx, MIAIE_EINVAL, "gemm_i8: M too large for the 64x64 fallback");

@@ -67,6 +67,23 @@ def test_gemm_i8_single_tile_config(ctx):
     assert np.array_equal(Cg, oracle.gemm_i8(A, B))
 
 
+@pytest.mark.parametrize("shape,layout", [((512, 384, 128), mi.B_NN), ((512, 384, 192), mi.B_NT),
+                                          ((4096, 4096, 128), mi.B_NN), ((4096, 4096, 128), mi.B_NT),
+                                          ((2048, 1024, 256), mi.B_NN)])
+def test_gemm_i8_pipeline_tile_widths(ctx, shape, layout):
+    """Shapes that select the 128-wide (N % 256 != 0, or a grid under one round
+    of CUs) and the 256-wide (4096^2 grid) pipelined tiles, both B layouts."""
+    M, N, K = shape
+    _say("gemm_i8 pipeline widths", shape, layout)
+    rng = np.random.default_rng(M + N + K + layout)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(N, K) if layout == mi.B_NT else (K, N), dtype=np.int8)
+    Yg, Cg = _run_gemm_i8(ctx, A, B, layout, 9, False)
+    Yo, Co = oracle.gemm_i8_rq(A, B, 9, b_nt=layout == mi.B_NT, want_acc=True)
+    assert np.array_equal(Cg, Co)
+    assert np.array_equal(Yg, Yo)
+
+
 @pytest.mark.parametrize("shape", [(64, 64, 64), (100, 50, 300), (256, 256, 64), (512, 512, 512)])
 @pytest.mark.parametrize("shift,relu", [(10, False), (11, True), (0, False), (1, False), (31, False), (7, True)])
 def test_gemm_i8_rq(ctx, shape, shift, relu):
