@@ -2,7 +2,8 @@
 
 Compiles every aiehlc_amd/csrc/*.hip translation unit with hipcc for gfx950
 and links them into aiehlc_amd/lib/libmiaie.so, then builds the C++ harness
-programs in aiehlc_amd/harness/ against it.  Runs on a machine without a GPU
+programs in aiehlc_amd/harness/ against it and the measurement probes in
+aiehlc_amd/probes/.  Runs on a machine without a GPU
 (hipcc cross-compiles).
 
 Flags: -O3, C++17, hidden visibility (only the MIAIE_API symbols of
@@ -66,6 +67,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB)
     build_harness(verbose)
+    build_probes(verbose)
     return LIB
 
 
@@ -80,6 +82,19 @@ def build_harness(verbose: bool = False) -> None:
                os.path.join(HARNESS, f), "-o", exe + ".tmp", f"-L{LIBDIR}", "-lmiaie",
                "-Wl,-rpath,$ORIGIN/../lib"]
         _run(cmd, verbose)
+        os.replace(exe + ".tmp", exe)
+
+
+def build_probes(verbose: bool = False) -> None:
+    """Standalone measurement programs (aiehlc_amd/probes/*.hip) used by bench.py."""
+    pdir = os.path.join(HERE, "probes")
+    if not os.path.isdir(pdir):
+        return
+    for f in sorted(os.listdir(pdir)):
+        if not f.endswith(".hip"):
+            continue
+        exe = os.path.join(pdir, f[:-4])
+        _run([HIPCC, *HIP_FLAGS, os.path.join(pdir, f), "-o", exe + ".tmp"], verbose)
         os.replace(exe + ".tmp", exe)
 
 

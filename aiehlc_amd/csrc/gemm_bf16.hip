@@ -18,7 +18,10 @@ namespace {
 
 namespace dev = miaie::dev;
 
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// 64-byte LDS rows: chunk c of row r at chunk c ^ swz(r).  gfx950 serves a
+// ds_read_b128 16 lanes at a time from 64 four-byte banks; XOR with row
+// bits 2-3 puts the 16 rows one fragment read touches on distinct banks.
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + ((chunk ^ swz(row)) << 4); }
 
 __device__ __forceinline__ v8bf as_bf(v4i x) { return __builtin_bit_cast(v8bf, x); }

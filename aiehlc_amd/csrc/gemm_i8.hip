@@ -56,12 +56,13 @@ struct Requant {
   }
 };
 
-// LDS tile rows are 64 bytes = four 16-byte chunks.  The chunk index is
-// XOR-swizzled with bits of the row so that (a) 16 or 8 consecutive rows
-// read at one logical chunk (the MFMA fragment pattern), (b) 4 rows x 4
-// chunks (the A store pattern) and (c) the rotated transposed-B store
-// pattern all fall on distinct banks, for 32- and 64-bank LDS alike.
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// LDS tile rows are 64 bytes = four 16-byte chunks; chunk c of row r is
+// stored at chunk c ^ swz(r).  gfx950 serves a ds_read_b128 16 lanes at a
+// time from 64 four-byte banks; the MFMA fragment read has lanes 0..15 on
+// 16 consecutive rows at one logical chunk, and XOR with row bits 2-3 makes
+// those 16 reads cover all 64 banks (measured conflict-free with
+// SQ_LDS_BANK_CONFLICT; XOR with row bits 1-2 measured 2-way conflicts).
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + ((chunk ^ swz(row)) << 4); }
 
 // ---------------------------------------------------------- pipelined tile

@@ -1,19 +1,25 @@
 #!/usr/bin/env python3
-"""Benchmark: int8 GEMM + requant at M=N=K=4096 on one MI355X (BASELINE config 2).
+"""Benchmark: int8 GEMM + requant at M=N=K=4096 on one MI355X.
 
-One step = one miaie_gemm_i8_rq launch (A 4096x4096 int8 NN B 4096x4096 int8,
-int32 accumulate, Y = sat_int8((acc + 2^9) >> 10)) over inputs already
-resident in HBM.  W untimed warm-up steps, then K timed steps bracketed by a
-stream drain on both sides and HIP events on the stream the kernel is
-launched on.  Prints ONE JSON line.
+One step = one miaie_gemm_i8_rq launch: A 4096x4096 int8 times B 4096x4096
+int8, both row-major (NN), int32 accumulate, Y = sat_int8((acc + 2^9) >> 10),
+over inputs already resident in HBM.  W untimed warm-up steps, then K timed
+steps bracketed by a drain of the context stream on both sides, timed with
+HIP events recorded on that same stream.  Prints ONE JSON line.
 
-Extras in the same line (not the headline): the 3x3 int8 conv2d of config 4
-(GOPS), the bf16 8192^3 GEMM of config 3 and the int8 MLP of config 5.
+Also in the line (not the headline):
+  extras.conv2d_3x3      int8 3x3 conv2d, N=8 56x56 Cin=Cout=64 (GOPS, roofline)
+  extras.gemm_bf16_8192  bf16 8192^3 GEMM, fp32 accumulate/output (TFLOP/s)
+  extras.mlp_i8          chained int8 MLP 2048x4096 -> 11008 -> 4096 (TOP/s)
+  extras.mfma_ceiling    register-only MFMA rate on this GPU, constant and
+                         random operands (aiehlc_amd/probes/mfma_ceiling)
+  cpu_baseline           the reference's CPU golden loop (i-j-k, int32
+                         accumulate, B in the [N][K] layout of
+                         example/matrixmultiply/aieml_mm.cc:194-230), restated
+                         in oracle/miaie_oracle.c, on this host's cores
 
-cpu_baseline: the reference's CPU golden loop (i-j-k, int32 accumulate, B in
-the reference's [N][K] layout: example/matrixmultiply/aieml_mm.cc:217-223),
-restated in oracle/miaie_oracle.c, timed on this host on a row slab of the
-same 4096^3 problem.
+roofline.traffic is read from profiles/gemm_i8_rq_4096_traffic.txt, which
+records the rocprofv3 FETCH_SIZE / WRITE_SIZE runs it comes from.
 """
 from __future__ import annotations
 
@@ -21,6 +27,8 @@ import argparse
 import ctypes as C
 import json
 import os
+import re
+import subprocess
 import sys
 import time
 
@@ -29,14 +37,17 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, TOP/s
-PEAK_BF16_TFLOPS = 2500.0    # dense bf16
+# MI355X published dense peaks
+PEAK_INT8_TOPS = 5000.0
+PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_rq_4096_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_rq_4096_traffic.txt")
+CEILING_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "mfma_ceiling")
+METRIC = "int8 GEMM TOPS (% MFMA peak) at 4096^3; int8 conv2d 3x3 GOPS; vs host CPU"
 
 
 class HipTimer:
-    """hipEvent pair on a given stream (the miaie context's stream)."""
+    """hipEvent pair recorded on a given stream (the miaie context's stream)."""
 
     def __init__(self, stream: int):
         self.hip = C.CDLL("libamdhip64.so")
@@ -61,6 +72,7 @@ class HipTimer:
 
 
 def timed(ctx, timer, fn, steps: int, warmup: int) -> float:
+    """Average ms per call over `steps` back-to-back calls, after `warmup`."""
     for _ in range(warmup):
         fn()
     ctx.wait(120_000)
@@ -72,44 +84,70 @@ def timed(ctx, timer, fn, steps: int, warmup: int) -> float:
     return ms / steps
 
 
+def read_traffic() -> tuple[int | None, str | None]:
+    """HBM bytes per launch recorded in the committed rocprofv3 summary."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None, None
+    text = open(TRAFFIC_FILE).read()
+    m = re.search(r"^hbm_bytes_per_launch:\s*(\d+)", text, re.M)
+    return (int(m.group(1)) if m else None), os.path.relpath(TRAFFIC_FILE, ROOT)
+
+
 def cpu_baseline(seconds: float) -> dict:
-    """Reference golden loop on the host: rows slab of the 4096^3 problem."""
+    """The reference golden loop on the host over the 4096^3 problem.
+
+    value: all of C with OpenMP over rows (threads = min(16, cores)).  Also a
+    single-thread slab and the reference host's -Os build on a slab."""
     import oracle
     from aiehlc_amd import synth
 
     M = N = K = 4096
     threads = min(16, os.cpu_count() or 1)
     A = synth.int8((M, K), 1)
-    B = synth.int8((K, N), 2)
-    Bt = np.ascontiguousarray(B.T)  # NN -> the reference's [N][K] layout, untimed
-    lib = oracle._lib()
+    Bt = np.ascontiguousarray(synth.int8((K, N), 2).T)  # NN -> the reference's [N][K] layout, untimed
     Cb = np.zeros((M, N), dtype=np.int32)
 
-    def run(rows, nt):
+    def run(lib, rows, nt):
         t0 = time.perf_counter()
         lib.oracle_gemm_i8_nt_rows(A.ctypes.data, Bt.ctypes.data, Cb.ctypes.data, M, N, K, K, K, N, 0, rows, nt)
         return time.perf_counter() - t0
 
-    probe_rows = threads * 2
-    t = run(probe_rows, threads)
-    rows = int(min(M, max(probe_rows, probe_rows * seconds / max(t, 1e-3))))
-    rows -= rows % threads or 0
+    lib = oracle._lib()
+    # size the multi-threaded sample to about `seconds` of wall time (capped at all of C)
+    probe = max(threads, 64)
+    t = run(lib, probe, threads)
+    rows = int(min(M, max(probe, probe * seconds / max(t, 1e-3))))
+    rows -= rows % threads
     rows = max(rows, threads)
-    t = run(rows, threads)
+    t = run(lib, rows, threads)
     tops = 2.0 * rows * N * K / t / 1e12
-    t1 = run(8, 1)
-    tops1 = 2.0 * 8 * N * K / t1 / 1e12
+    t1 = run(lib, 16, 1)
+    tops1 = 2.0 * 16 * N * K / t1 / 1e12
+    t_os = run(oracle._lib("liboracle_os.so"), 16, 1)
+    tops_os = 2.0 * 16 * N * K / t_os / 1e12
     return {
         "value": round(tops, 6),
         "unit": "TOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"rows 0..{rows} of C (of 4096) of the 4096^3 int8 GEMM, reference i-j-k int32 loop "
-                  f"(aieml_mm.cc:217-223) on int8 operands, B transposed to [N][K] untimed, gcc -O2, "
-                  f"OpenMP over rows, {t:.2f}s",
+        "sample": f"rows 0..{rows} of C (of 4096) of the 4096^3 int8 GEMM: the reference's i-j-k int32 golden "
+                  f"loop (aieml_mm.cc:194-230) on int8 operands, B transposed to [N][K] untimed, gcc -O2 "
+                  f"-fopenmp over rows, {threads} threads, {t:.2f} s wall ({t * threads:.1f} thread-s); no requant",
         "single_thread_value": round(tops1, 6),
-        "requant_in_loop": False,
+        "single_thread_sample": f"rows 0..16, 1 thread, gcc -O2, {t1:.2f} s",
+        "single_thread_Os_value": round(tops_os, 6),
+        "single_thread_Os_sample": f"rows 0..16, 1 thread, gcc -Os (the reference host's flag, script/aiehlc.sh:343), "
+                                   f"{t_os:.2f} s",
     }
+
+
+def mfma_ceiling() -> dict | None:
+    if not os.path.exists(CEILING_EXE):
+        return None
+    r = subprocess.run([CEILING_EXE], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        return {"error": r.stderr.strip()[-300:]}
+    return json.loads(r.stdout)
 
 
 def main() -> int:
@@ -124,8 +162,8 @@ def main() -> int:
                     help="only run miaie_copy_d2d of MIB MiB, --steps times (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md and not run", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "how the GEMM, conv and MLP would shard over several GPUs is described, not run", file=sys.stderr)
         return 2
 
     import aiehlc_amd as mi
@@ -141,27 +179,24 @@ def main() -> int:
                           "GBps_read_plus_write": round(2 * nb / (ms * 1e-3) / 1e9, 1)}), flush=True)
         ctx.close()
         return 0
+
+    # ---- headline: int8 GEMM + requant, 4096^3 NN, shift 10
     M = N = K = 4096
     dA, dB, dY = ctx.empty((M, K), np.int8), ctx.empty((K, N), np.int8), ctx.empty((M, N), np.int8)
     ctx.fill_i8(dA, M * K, 1)
     ctx.fill_i8(dB, K * N, 2)
     ctx.wait(60_000)
-
-    def step():
-        ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, mi.B_NN)
-
-    ms = timed(ctx, timer, step, args.steps, args.warmup)
+    ms = timed(ctx, timer, lambda: ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, mi.B_NN),
+               args.steps, args.warmup)
     ops = 2.0 * M * N * K
     tops = ops / (ms * 1e-3) / 1e12
-
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    for b in (dA, dB, dY):
+        b.free()
+    traffic, traffic_src = read_traffic()
 
     extras = {}
     if not args.no_extras:
-        # config 4: conv2d 3x3
+        # config 4: int8 conv2d 3x3
         Nb, H, W, Ci, Co = 8, 56, 56, 64, 64
         dX, dW, dS, dYc = (ctx.empty((Nb, H, W, Ci), np.int8), ctx.empty((Co, 3, 3, Ci), np.int8),
                            ctx.upload(mi.synth.shifts(Co, 7)), ctx.empty((Nb, H, W, Co), np.int8))
@@ -171,29 +206,32 @@ def main() -> int:
                      max(args.steps, 200), args.warmup)
         conv_ops = 2.0 * Nb * H * W * Co * Ci * 9
         conv_bytes = Nb * H * W * Ci + Co * 9 * Ci + Co + Nb * H * W * Co
+        roof = min(PEAK_INT8_TOPS, conv_ops / conv_bytes * PEAK_HBM_GBS / 1e3)
         extras["conv2d_3x3"] = {
-            "config": "N=8 H=W=56 Cin=Cout=64 3x3 s1 p1 NHWC/OHWI, per-channel shift",
+            "config": "N=8 H=W=56 Cin=Cout=64 3x3 stride 1 pad 1, NHWC x OHWI, per-channel shift in [8,12]",
+            "kernel": "conv2d_i8_rows<3,3,64>",
             "us_per_step": round(ms_c * 1e3, 3),
             "gops": round(conv_ops / (ms_c * 1e-3) / 1e9, 1),
             "alg_GBps": round(conv_bytes / (ms_c * 1e-3) / 1e9, 1),
-            "roof_tops": round(min(PEAK_INT8_TOPS, conv_ops / conv_bytes * PEAK_HBM_GBS / 1e3), 1),
-            "frac_of_roof": round(conv_ops / (ms_c * 1e-3) / 1e12 / min(PEAK_INT8_TOPS, conv_ops / conv_bytes * PEAK_HBM_GBS / 1e3), 4),
-            "note": "events bracket back-to-back launches: includes launch gaps; inputs L2/MALL-hot",
+            "roofline": {"bound": "hbm", "alg_bytes": conv_bytes, "roof_tops": round(roof, 1),
+                         "frac": round(conv_ops / (ms_c * 1e-3) / 1e12 / roof, 4)},
+            "note": "events bracket back-to-back launches, so us_per_step includes the gap between launches",
         }
         for b in (dX, dW, dS, dYc):
             b.free()
         # config 3: bf16 8192^3
         Mb = 8192
-        dAb, dBb, dCb = ctx.empty((Mb, Mb), np.uint16), ctx.empty((Mb, Mb), np.uint16), ctx.empty((Mb, Mb), np.float32)
+        dAb, dBb, dCb = (ctx.empty((Mb, Mb), np.uint16), ctx.empty((Mb, Mb), np.uint16),
+                         ctx.empty((Mb, Mb), np.float32))
         ctx.copy_h2d(dAb, mi.synth.bf16_normal((Mb, Mb), 1, 1.0 / np.sqrt(Mb)))
         ctx.copy_h2d(dBb, mi.synth.bf16_normal((Mb, Mb), 2, 1.0 / np.sqrt(Mb)))
         ms_b = timed(ctx, timer, lambda: ctx.gemm_bf16_f32(dAb, dBb, dCb, Mb, Mb, Mb), max(5, args.steps // 5), 2)
         tf = 2.0 * Mb ** 3 / (ms_b * 1e-3) / 1e12
-        extras["gemm_bf16_8192"] = {"ms_per_step": round(ms_b, 4), "tflops": round(tf, 1),
-                                    "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+        extras["gemm_bf16_8192"] = {"kernel": "gemm_bf16_tile256", "ms_per_step": round(ms_b, 4),
+                                    "tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
         for b in (dAb, dBb, dCb):
             b.free()
-        # config 5: MLP
+        # config 5: chained int8 MLP
         Mm, Km, Fm, Nm = 2048, 4096, 11008, 4096
         dXm, d1, d2 = ctx.empty((Mm, Km), np.int8), ctx.empty((Km, Fm), np.int8), ctx.empty((Fm, Nm), np.int8)
         dH, dYm = ctx.empty((Mm, Fm), np.int8), ctx.empty((Mm, Nm), np.int8)
@@ -203,13 +241,32 @@ def main() -> int:
         ms_m = timed(ctx, timer, lambda: ctx.mlp_i8(dXm, d1, d2, dH, dYm, Mm, Km, Fm, Nm, 11, 12),
                      max(5, args.steps // 2), 2)
         mops = 2.0 * 2 * Mm * Km * Fm
-        extras["mlp_i8"] = {"ms_per_step": round(ms_m, 4), "tops": round(mops / (ms_m * 1e-3) / 1e12, 1),
+        extras["mlp_i8"] = {"kernel": "gemm_i8_pipe<128> x 2", "ms_per_step": round(ms_m, 4),
+                            "tops": round(mops / (ms_m * 1e-3) / 1e12, 1),
                             "frac_of_peak": round(mops / (ms_m * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
         for b in (dXm, d1, d2, dH, dYm):
             b.free()
+    ctx.close()
+    if not args.no_extras:
+        extras["mfma_ceiling"] = mfma_ceiling()
 
+    roofline = {
+        "bound": "mfma",
+        "kernel": "gemm_i8_pipe<256, NN, Y>",
+        "achieved": round(tops, 2),
+        "peak": PEAK_INT8_TOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tops / PEAK_INT8_TOPS, 4),
+        "traffic": traffic,
+        "traffic_source": traffic_src,
+        "alg_ops_per_launch": ops,
+        "alg_bytes_per_launch": M * K + K * N + M * N,
+    }
+    ceil = extras.get("mfma_ceiling") or {}
+    if isinstance(ceil.get("i8_32x32x32_random"), dict):
+        roofline["frac_of_measured_random_operand_ceiling"] = round(tops / ceil["i8_32x32x32_random"]["tops"], 4)
     line = {
-        "metric": "int8 GEMM TOPS (% MFMA peak) at 4096^3; int8 conv2d 3x3 GOPS; vs host CPU",
+        "metric": METRIC,
         "value": round(tops, 2),
         "unit": "TOP/s",
         "n_gpus": 1,
@@ -223,23 +280,10 @@ def main() -> int:
         "data": "synthetic (SplitMix64-seeded int8, generated on the device)",
         "config": {"workload": "int8 GEMM + requant, M=N=K=4096, A and B row-major (NN), int32 accumulate, "
                                "Y = sat_int8((acc + 2^9) >> 10)", "M": M, "N": N, "K": K, "shift": 10},
-        "roofline": {
-            "bound": "mfma",
-            "kernel": "gemm_i8_tile256<NN, Y>",
-            "achieved": round(tops, 2),
-            "peak": PEAK_INT8_TOPS,
-            "unit": "TOP/s",
-            "frac": round(tops / PEAK_INT8_TOPS, 4),
-            "traffic": traffic,
-            "alg_bytes_per_launch": M * K + K * N + M * N,
-        },
+        "roofline": roofline,
         "extras": extras,
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_seconds),
     }
-    ctx.close()
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-    else:
-        line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
     return 0
 
