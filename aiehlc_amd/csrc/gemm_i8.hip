@@ -208,11 +208,16 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
       return v4i{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
   };
 
+  // When only the requantized output is wanted, the accumulators start at
+  // the rounding term 2^(shift-1) so the epilogue needs no add.
+  const int rnd = shift ? 1 << (shift - 1) : 0;
+  const int acc0 = (WRITE_Y && !WRITE_C) ? rnd : 0;
   v16i acc[4][G::NJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < G::NJ; ++j) acc[i][j] = v16i{0};
+    for (int j = 0; j < G::NJ; ++j)
+      acc[i][j] = v16i{acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0};
 
   const int KT = K / BK;
   constexpr int CP = G::CP_PER_TILE;
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
     // 16-byte stores.  Every LDS read and copy of the main loop completed
     // before its last barrier.
     constexpr int CH = BN / 16;
-    const Requant rq{shift, shift ? 1 << (shift - 1) : 0, relu ? 0 : -128, 127};
+    const Requant rq{shift, rnd - acc0, relu ? 0 : -128, 127};
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -447,12 +452,12 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
 }
 
 // Tile width for the pipelined kernel: 256 unless 128-wide tiles finish the
-// grid in fewer rounds of 256 workgroups (one per CU), counting a 128-wide
-// tile as 0.55 of a 256-wide one.  0: neither fits the shape.
-int pick_bn(int M, int N) {
+// grid in fewer rounds of workgroups (one per CU), counting a 128-wide tile
+// as 0.55 of a 256-wide one.  0: neither fits the shape.
+int pick_bn(int M, int N, int cus) {
   if (M % BM != 0) return 0;
-  const long rounds256 = N % 256 == 0 ? ((long)(M / BM) * (N / 256) + 255) / 256 : -1;
-  const long rounds128 = N % 128 == 0 ? ((long)(M / BM) * (N / 128) + 255) / 256 : -1;
+  const long rounds256 = N % 256 == 0 ? ((long)(M / BM) * (N / 256) + cus - 1) / cus : -1;
+  const long rounds128 = N % 128 == 0 ? ((long)(M / BM) * (N / 128) + cus - 1) / cus : -1;
   if (rounds256 < 0) return rounds128 < 0 ? 0 : 128;
   if (rounds128 < 0) return 256;
   return rounds128 * 55 < rounds256 * 100 ? 128 : 256;
@@ -468,7 +473,7 @@ int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, 
   // The 256x256 kernel copies 16-byte chunks (16-byte aligned operands and
   // strides), keeps per-lane offsets of up to 64 rows in 32 bits, and its
   // requant shortcut needs K < 2^16.
-  const int bn = pick_bn(M, N);
+  const int bn = pick_bn(M, N, ctx->cus);
   const bool big = bn != 0 && (K % BK == 0) && (!Y || K < (1 << 16)) && aligned(A, 16) &&
                    aligned(B, 16) && lda % 16 == 0 && ldb % 16 == 0 && lda < (1 << 25) && ldb < (1 << 25) &&
                    (!Y || (aligned(Y, 16) && ldy % 16 == 0)) && (!C || (aligned(C, 16) && ldc % 4 == 0));

@@ -14,6 +14,7 @@ struct miaie_ctx {
   hipStream_t stream = nullptr;
   bool own_stream = false;
   hipEvent_t done = nullptr;  // recorded by miaie_wait
+  int cus = 256;              // compute units of the device (grid sizing of persistent kernels)
   char err[512] = {0};
 };
 

@@ -119,6 +119,7 @@ extern "C" int miaie_init_on_stream(miaie_ctx** out, int device, void* stream) {
   miaie_ctx* ctx = new (std::nothrow) miaie_ctx();
   if (!ctx) return fail(nullptr, MIAIE_ENOMEM, "miaie_init: host allocation failed");
   ctx->device = device;
+  ctx->cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
   if (stream) {
     ctx->stream = static_cast<hipStream_t>(stream);
   } else {
