@@ -157,8 +157,8 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
 // Each of the 8 waves then owns 32 output pixels x 32 channels and runs the
 // whole k = (r, s, ci) reduction from LDS (one v_mfma_i32_32x32x32_i8 per
 // 32-wide k-step, fully unrolled), so there is no im2col buffer and no
-// cross-wave reduction.  The int8 results are staged in LDS and leave as
-// contiguous NHWC rows.
+// cross-wave reduction.  The requantized int8 results are stored straight from
+// registers, one dword (4 channels of a pixel) per store.
 constexpr int ROWS = 2;   // output rows per workgroup
 constexpr int PB = 64;    // output columns per row (padded)
 constexpr int RCOB = 64;  // output channels per workgroup
@@ -179,7 +179,7 @@ struct RowsGeom {
   static constexpr int X_BYTES = XR * XC * CIN;
   static constexpr int LDS = X_BYTES + RCOB * WP;
   static constexpr int T = R * S * CIN / 32;                // 32-wide k-steps
-  static_assert(LDS <= 65536 && ROWS * PB * RCOB <= LDS, "row-pair conv LDS budget");
+  static_assert(LDS <= 65536, "row-pair conv LDS budget");
 };
 
 template <int R, int S, int CIN>
@@ -196,6 +196,13 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   const int co0 = blockIdx.y * RCOB;
   int8_t* const xs = smem;
   int8_t* const ws = smem + G::X_BYTES;
+
+  // this lane's 16 output channels' shifts (4 per dword), loaded up front so
+  // their latency hides under the staging
+  const int wc_ = wave & 1, fh_ = lane >> 5;
+  uint32_t sh4[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) sh4[g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc_ + 8 * g + 4 * fh_);
 
   // ---- stage X (zero outside the image) and W: all loads first, then the LDS writes
   v4i xv[G::XQ], wv[G::WQ];
@@ -246,33 +253,20 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
     acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, xf, acc, 0, 0, 0);
   }
 
-  // ---- requant (per channel) and stage [row][px][64 ch] in LDS.
-  // acc[4g + tt]: channel 32wc + 8g + 4*(lane/32) + tt, pixel px.
-  uint32_t sh4[4];
+  // ---- requant (per channel) and store.  acc[4g + tt]: channel
+  // 32wc + 8g + 4*(lane/32) + tt, pixel px: four consecutive channels of one
+  // pixel per dword, written straight from registers (no LDS round trip, no
+  // barrier).
+  const int ho = ho0 + rr;
+  if (ho < Ho && px < Wo) {
+    int8_t* const y = Y + (((size_t)n * Ho + ho) * Wo + px) * Cout + co0 + 32 * wc + 4 * fh;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) sh4[g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc + 8 * g + 4 * fh);
-  __syncthreads();  // all fragment reads done before the staging overwrites X
-  int8_t* const os = smem;
+    for (int g = 0; g < 4; ++g) {
+      uint32_t packed = 0;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int cc = 32 * wc + 8 * g + 4 * fh;
-    uint32_t packed = 0;
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-      packed |= (uint32_t)(requant1(acc[4 * g + tt], (sh4[g] >> (8 * tt)) & 0xFF) & 0xFF) << (8 * tt);
-    const int off = (rr * PB + px) * RCOB + ((((cc >> 4) ^ ((px >> 2) & 3))) << 4) + (cc & 15);
-    *reinterpret_cast<uint32_t*>(os + off) = packed;
-  }
-  __syncthreads();
-  // ---- copy out: (row, pixel, 16-byte chunk) per thread
-#pragma unroll
-  for (int u = 0; u < ROWS * PB * 4 / 512; ++u) {
-    const int q = tid + 512 * u;
-    const int c = q & 3, p = (q >> 2) % PB, row = q / (4 * PB);
-    const int ho = ho0 + row;
-    if (ho < Ho && p < Wo) {
-      const v4i v = *reinterpret_cast<const v4i*>(os + (row * PB + p) * RCOB + ((c ^ ((p >> 2) & 3)) << 4));
-      *reinterpret_cast<v4i*>(Y + (((size_t)n * Ho + ho) * Wo + p) * Cout + co0 + 16 * c) = v;
+      for (int tt = 0; tt < 4; ++tt)
+        packed |= (uint32_t)(requant1(acc[4 * g + tt], (sh4[g] >> (8 * tt)) & 0xFF) & 0xFF) << (8 * tt);
+      *reinterpret_cast<uint32_t*>(y + 8 * g) = packed;
     }
   }
 }
