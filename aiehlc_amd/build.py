@@ -1,8 +1,10 @@
 """Build step for the miaie HIP library (gfx950 only).
 
 Compiles every aiehlc_amd/csrc/*.hip translation unit with hipcc for gfx950
-and links them into aiehlc_amd/lib/libmiaie.so, then builds the C++ harness
-programs in aiehlc_amd/harness/ against it and the measurement probes in
+and links them into aiehlc_amd/lib/libmiaie.so, builds the aie-rt-shaped
+facade aiehlc_amd/csrc/xaie/*.hip into aiehlc_amd/lib/libmiaie_xaie.so on top
+of it, then the harness programs in aiehlc_amd/harness/ (C++ against
+miaie.hpp, C against miaie_xaie.h) and the measurement probes in
 aiehlc_amd/probes/.  Runs on a machine without a GPU
 (hipcc cross-compiles).
 
@@ -24,6 +26,8 @@ OBJ = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libmiaie.so")
 HARNESS = os.path.join(HERE, "harness")
+XAIE_SRC = os.path.join(CSRC, "xaie")
+XAIE_LIB = os.path.join(LIBDIR, "libmiaie_xaie.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -66,21 +70,43 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB)
+    build_xaie(verbose)
     build_harness(verbose)
     build_probes(verbose)
     return LIB
+
+
+def build_xaie(verbose: bool = False) -> str:
+    """libmiaie_xaie.so: the aie-rt-shaped facade (include/miaie_xaie.h), a
+    client of libmiaie.so with its own tile-array kernels."""
+    srcs = sorted(os.path.join(XAIE_SRC, f) for f in os.listdir(XAIE_SRC) if f.endswith(".hip"))
+    objs = [os.path.join(OBJ, "xaie_" + os.path.basename(s)[:-4] + ".o") for s in srcs]
+    for s, o in zip(srcs, objs):
+        _run([HIPCC, *HIP_FLAGS, "-c", s, "-o", o], verbose)
+    tmp = XAIE_LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, f"-L{LIBDIR}", "-lmiaie",
+          "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp, XAIE_LIB)
+    return XAIE_LIB
 
 
 def build_harness(verbose: bool = False) -> None:
     if not os.path.isdir(HARNESS):
         return
     for f in sorted(os.listdir(HARNESS)):
-        if not f.endswith(".cpp"):
+        if f.endswith(".cpp"):
+            exe = os.path.join(HARNESS, f[:-4])
+            cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}",
+                   os.path.join(HARNESS, f), "-o", exe + ".tmp", f"-L{LIBDIR}", "-lmiaie",
+                   "-Wl,-rpath,$ORIGIN/../lib"]
+        elif f.endswith(".c"):
+            # C programs written against the aie-rt-shaped facade
+            exe = os.path.join(HARNESS, f[:-2])
+            cmd = ["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}",
+                   os.path.join(HARNESS, f), "-o", exe + ".tmp", f"-L{LIBDIR}", "-lmiaie_xaie", "-lmiaie",
+                   "-Wl,-rpath,$ORIGIN/../lib"]
+        else:
             continue
-        exe = os.path.join(HARNESS, f[:-4])
-        cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}",
-               os.path.join(HARNESS, f), "-o", exe + ".tmp", f"-L{LIBDIR}", "-lmiaie",
-               "-Wl,-rpath,$ORIGIN/../lib"]
         _run(cmd, verbose)
         os.replace(exe + ".tmp", exe)
 
