@@ -13,6 +13,8 @@ Also in the line (not the headline):
   extras.mlp_i8          chained int8 MLP 2048x4096 -> 11008 -> 4096 (TOP/s)
   extras.mfma_ceiling    register-only MFMA rate on this GPU, constant and
                          random operands (aiehlc_amd/probes/mfma_ceiling)
+  extras.vendor_library  the same int8 4096^3 and bf16 8192^3 products through
+                         hipBLASLt (torch._int_mm / torch.matmul) on this GPU
   cpu_baseline           the reference's CPU golden loop (i-j-k, int32
                          accumulate, B in the [N][K] layout of
                          example/matrixmultiply/aieml_mm.cc:194-230), restated
@@ -150,6 +152,52 @@ def mfma_ceiling() -> dict | None:
     return json.loads(r.stdout)
 
 
+def vendor_library(steps: int) -> dict:
+    """The same GEMMs through ROCm's libraries (hipBLASLt behind torch), on
+    the same GPU in the same process: the bar a tuned vendor kernel sets
+    under the same clocks.  Timed with torch's events on torch's stream."""
+    try:
+        import torch
+    except Exception as ex:  # torch is plumbing here; report and carry on
+        return {"error": repr(ex)[:200]}
+    dev = torch.device("cuda:0")
+
+    def t_ms(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    out = {"library": "torch " + torch.__version__ + " (hipBLASLt)"}
+    try:
+        M = 4096
+        g = torch.Generator(device=dev)
+        g.manual_seed(5)
+        A = torch.randint(-128, 128, (M, M), dtype=torch.int8, device=dev, generator=g)
+        B = torch.randint(-128, 128, (M, M), dtype=torch.int8, device=dev, generator=g)
+        Bc = B.t().contiguous().t()  # same matrix, column-major storage
+        for name, b in (("int8_4096_rowmajor_B", B), ("int8_4096_colmajor_B", Bc)):
+            ms = t_ms(lambda: torch._int_mm(A, b), steps)
+            out[name] = {"op": "torch._int_mm (int32 out)", "tops": round(2.0 * M ** 3 / (ms * 1e-3) / 1e12, 1)}
+        del A, B, Bc
+        Mb = 8192
+        a = torch.randn(Mb, Mb, device=dev, generator=g).to(torch.bfloat16)
+        b = torch.randn(Mb, Mb, device=dev, generator=g).to(torch.bfloat16)
+        ms = t_ms(lambda: torch.matmul(a, b), max(5, steps // 5))
+        out["bf16_8192"] = {"op": "torch.matmul (bf16 out)", "tflops": round(2.0 * Mb ** 3 / (ms * 1e-3) / 1e12, 1)}
+        del a, b
+        torch.cuda.empty_cache()
+    except Exception as ex:
+        out["error"] = repr(ex)[:300]
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +297,7 @@ def main() -> int:
     ctx.close()
     if not args.no_extras:
         extras["mfma_ceiling"] = mfma_ceiling()
+        extras["vendor_library"] = vendor_library(args.steps)
 
     roofline = {
         "bound": "mfma",
