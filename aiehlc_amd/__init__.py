@@ -75,6 +75,10 @@ _SIGS = {
     "miaie_conv2d_i8_nhwc": (_i, [_p, _p, _p, _p, _p] + [_i] * 9),
     "miaie_mlp_i8": (_i, [_p, _p, _p, _p, _p, _p] + [_i] * 6),
     "miaie_fill_i8": (_i, [_p, _p, _sz, _u64]),
+    "miaie_graph_begin": (_i, [_p]),
+    "miaie_graph_end": (_i, [_p, C.POINTER(_p)]),
+    "miaie_graph_launch": (_i, [_p, _p]),
+    "miaie_graph_destroy": (_i, [_p]),
     "miaie_version": (C.c_char_p, []),
 }
 
@@ -128,6 +132,43 @@ def _addr(x) -> int | None:
     if isinstance(x, DeviceBuffer):
         return x.ptr
     return int(x)
+
+
+class Graph:
+    """A recorded chain of entry points (miaie_graph_*), replayed by launch()."""
+
+    def __init__(self, ctx: "Context"):
+        self.ctx = ctx
+        self.handle = None
+
+    def launch(self) -> None:
+        if not self.handle:
+            raise MiaieError(MIAIE_EINVAL, "graph is not recorded yet")
+        self.ctx._call("miaie_graph_launch", self.handle)
+
+    def destroy(self) -> None:
+        if self.handle:
+            self.ctx.lib.miaie_graph_destroy(self.handle)
+            self.handle = None
+
+
+class _Recording:
+    def __init__(self, ctx: "Context"):
+        self.ctx = ctx
+        self.graph = Graph(ctx)
+
+    def __enter__(self) -> Graph:
+        self.ctx._call("miaie_graph_begin")
+        return self.graph
+
+    def __exit__(self, exc_type, *exc):
+        h = _p()
+        rc = self.ctx.lib.miaie_graph_end(self.ctx.handle, C.byref(h) if exc_type is None else None)
+        if exc_type is None:
+            if rc != MIAIE_OK:
+                raise MiaieError(rc, self.ctx.last_error())
+            self.graph.handle = h.value
+        return False
 
 
 class Context:
@@ -221,6 +262,11 @@ class Context:
 
     def fill_i8(self, buf, n: int, tensor_id: int) -> None:
         self._call("miaie_fill_i8", _addr(buf), _sz(n), _u64(tensor_id))
+
+    def record(self) -> _Recording:
+        """`with ctx.record() as g: <entry points>` records them into g
+        instead of running them; g.launch() replays the chain."""
+        return _Recording(self)
 
     # -- reference kernels
     def mm_window_i32(self, win, out, n: int) -> None:

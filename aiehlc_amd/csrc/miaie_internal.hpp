@@ -15,6 +15,7 @@ struct miaie_ctx {
   bool own_stream = false;
   hipEvent_t done = nullptr;  // recorded by miaie_wait
   int cus = 256;              // compute units of the device (grid sizing of persistent kernels)
+  bool recording = false;     // between miaie_graph_begin and miaie_graph_end
   char err[512] = {0};
 };
 
@@ -31,6 +32,10 @@ int enter(miaie_ctx* ctx);
 
 // Check the launch that was just queued.
 int check_launch(miaie_ctx* ctx, const char* kernel);
+
+// Entry points that wait for the device or allocate start with this: they
+// cannot be recorded into a graph.
+int refuse_while_recording(miaie_ctx* ctx, const char* what);
 
 __host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 

@@ -46,6 +46,12 @@ int check_launch(miaie_ctx* ctx, const char* kernel) {
   return MIAIE_OK;
 }
 
+int refuse_while_recording(miaie_ctx* ctx, const char* what) {
+  if (ctx->recording)
+    return fail(ctx, MIAIE_EINVAL, "%s: not allowed while a graph is being recorded (miaie_graph_begin)", what);
+  return MIAIE_OK;
+}
+
 }  // namespace miaie
 
 using namespace miaie;
@@ -155,6 +161,12 @@ extern "C" int miaie_finish(miaie_ctx* ctx) {
   if (!ctx) return MIAIE_OK;
   int rc = MIAIE_OK;
   (void)hipSetDevice(ctx->device);
+  if (ctx->recording) {  // abandon an unfinished recording
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(ctx->stream, &g);
+    if (g) (void)hipGraphDestroy(g);
+    ctx->recording = false;
+  }
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) rc = MIAIE_EHIP;
   if (ctx->done) (void)hipEventDestroy(ctx->done);
@@ -179,6 +191,7 @@ extern "C" int miaie_get_stream(miaie_ctx* ctx, void** stream) {
 extern "C" int miaie_alloc(miaie_ctx* ctx, size_t bytes, void** dev_ptr) {
   int rc = enter(ctx);
   if (rc) return rc;
+  if ((rc = refuse_while_recording(ctx, "miaie_alloc"))) return rc;
   MIAIE_CHECK_NOT_NULL(ctx, dev_ptr);
   *dev_ptr = nullptr;
   if (bytes == 0) return fail(ctx, MIAIE_EINVAL, "miaie_alloc: zero bytes");
@@ -190,6 +203,7 @@ extern "C" int miaie_alloc(miaie_ctx* ctx, size_t bytes, void** dev_ptr) {
 extern "C" int miaie_free(miaie_ctx* ctx, void* dev_ptr) {
   int rc = enter(ctx);
   if (rc) return rc;
+  if ((rc = refuse_while_recording(ctx, "miaie_free"))) return rc;
   if (!dev_ptr) return MIAIE_OK;
   hipError_t e = hipFree(dev_ptr);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");
@@ -199,6 +213,7 @@ extern "C" int miaie_free(miaie_ctx* ctx, void* dev_ptr) {
 extern "C" int miaie_copy_h2d(miaie_ctx* ctx, void* dst, const void* src, size_t bytes) {
   int rc = enter(ctx);
   if (rc) return rc;
+  if ((rc = refuse_while_recording(ctx, "miaie_copy_h2d"))) return rc;
   if (bytes == 0) return MIAIE_OK;
   MIAIE_CHECK_NOT_NULL(ctx, dst);
   MIAIE_CHECK_NOT_NULL(ctx, src);
@@ -212,6 +227,7 @@ extern "C" int miaie_copy_h2d(miaie_ctx* ctx, void* dst, const void* src, size_t
 extern "C" int miaie_copy_d2h(miaie_ctx* ctx, void* dst, const void* src, size_t bytes) {
   int rc = enter(ctx);
   if (rc) return rc;
+  if ((rc = refuse_while_recording(ctx, "miaie_copy_d2h"))) return rc;
   if (bytes == 0) return MIAIE_OK;
   MIAIE_CHECK_NOT_NULL(ctx, dst);
   MIAIE_CHECK_NOT_NULL(ctx, src);
@@ -248,6 +264,7 @@ extern "C" int miaie_copy_d2d(miaie_ctx* ctx, void* dst, const void* src, size_t
 extern "C" int miaie_wait(miaie_ctx* ctx, int timeout_ms) {
   int rc = enter(ctx);
   if (rc) return rc;
+  if ((rc = refuse_while_recording(ctx, "miaie_wait"))) return rc;
   hipError_t e = hipEventRecord(ctx->done, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
   if (timeout_ms < 0) {
@@ -287,3 +304,81 @@ extern "C" int miaie_fill_i8(miaie_ctx* ctx, int8_t* dst, size_t n, uint64_t ten
 }
 
 extern "C" const char* miaie_version(void) { return "miaie 0.1 (gfx950)"; }
+
+// ---------------------------------------------------------------- recorded chains
+struct miaie_graph {
+  int device = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  size_t nodes = 0;
+};
+
+extern "C" int miaie_graph_begin(miaie_ctx* ctx) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (ctx->recording) return fail(ctx, MIAIE_EINVAL, "miaie_graph_begin: already recording");
+  if (!ctx->stream)
+    return fail(ctx, MIAIE_EUNSUPPORTED, "miaie_graph_begin: the null stream cannot be recorded; use miaie_init");
+  hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamBeginCapture");
+  ctx->recording = true;
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_graph_end(miaie_ctx* ctx, miaie_graph** out) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (!ctx->recording) return fail(ctx, MIAIE_EINVAL, "miaie_graph_end: not recording (miaie_graph_begin)");
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+  ctx->recording = false;
+  if (e != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    return hip_fail(ctx, e, "hipStreamEndCapture");
+  }
+  if (!out) {
+    (void)hipGraphDestroy(g);
+    return fail(ctx, MIAIE_EINVAL, "miaie_graph_end: graph is NULL (the recording is discarded)");
+  }
+  *out = nullptr;
+  miaie_graph* mg = new miaie_graph;
+  mg->device = ctx->device;
+  mg->graph = g;
+  (void)hipGraphGetNodes(g, nullptr, &mg->nodes);
+  if (mg->nodes == 0) {
+    (void)hipGraphDestroy(g);
+    delete mg;
+    return fail(ctx, MIAIE_EINVAL, "miaie_graph_end: nothing was recorded");
+  }
+  e = hipGraphInstantiate(&mg->exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    delete mg;
+    return hip_fail(ctx, e, "hipGraphInstantiate");
+  }
+  *out = mg;
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_graph_launch(miaie_ctx* ctx, miaie_graph* graph) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  MIAIE_CHECK_NOT_NULL(ctx, graph);
+  if (ctx->recording) return fail(ctx, MIAIE_EINVAL, "miaie_graph_launch: cannot replay into a recording");
+  if (graph->device != ctx->device)
+    return fail(ctx, MIAIE_EINVAL, "miaie_graph_launch: graph recorded on device %d, context on %d", graph->device,
+                ctx->device);
+  hipError_t e = hipGraphLaunch(graph->exec, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphLaunch");
+  return MIAIE_OK;
+}
+
+extern "C" int miaie_graph_destroy(miaie_graph* graph) {
+  if (!graph) return MIAIE_OK;
+  (void)hipSetDevice(graph->device);
+  int rc = MIAIE_OK;
+  if (graph->exec && hipGraphExecDestroy(graph->exec) != hipSuccess) rc = MIAIE_EHIP;
+  if (graph->graph && hipGraphDestroy(graph->graph) != hipSuccess) rc = MIAIE_EHIP;
+  delete graph;
+  return rc;
+}

@@ -92,6 +92,30 @@ MIAIE_API int miaie_copy_d2d(miaie_ctx* ctx, void* dst_dev, const void* src_dev,
  * (timeout_ms < 0 waits without a deadline). */
 MIAIE_API int miaie_wait(miaie_ctx* ctx, int timeout_ms);
 
+/* ---- recorded kernel chains --------------------------------------------- */
+
+/* The reference chains kernels through the host: run k1, wait, move k1's
+ * output to k2's input tile, run k2, wait (example/multi/multi_tile.cpp:
+ * 110-140, seq_full_col.cpp:137-152).  Here a chain of entry points is
+ * recorded once as a HIP graph and replayed with one call: intermediates
+ * stay in device memory and no host step runs between kernels.
+ *
+ * miaie_graph_begin starts recording the context's stream.  Entry points
+ * called until miaie_graph_end are recorded, not run; the arguments
+ * (pointers, shapes) are fixed at recording time, while the buffers'
+ * contents are read at replay time.  While recording, entry points that
+ * wait for the device or allocate (miaie_copy_h2d, miaie_copy_d2h,
+ * miaie_wait, miaie_alloc, miaie_free) return MIAIE_EINVAL and record
+ * nothing.  A context created on the null stream cannot record
+ * (MIAIE_EUNSUPPORTED).  miaie_graph_launch queues one replay on the
+ * context's stream (asynchronous, like any launch). */
+typedef struct miaie_graph miaie_graph;
+MIAIE_API int miaie_graph_begin(miaie_ctx* ctx);
+MIAIE_API int miaie_graph_end(miaie_ctx* ctx, miaie_graph** graph);
+MIAIE_API int miaie_graph_launch(miaie_ctx* ctx, miaie_graph* graph);
+/* Waits for nothing: destroy a graph only once its replays have finished. */
+MIAIE_API int miaie_graph_destroy(miaie_graph* graph);
+
 /* ---- reference kernels (single AIE tile in the reference) -------------- */
 
 /* `mm` of example/matrixmultiply/aieml_mm.cc:41-93 and `perf` of
