@@ -75,6 +75,7 @@ _SIGS = {
     "miaie_conv2d_i8_nhwc": (_i, [_p, _p, _p, _p, _p] + [_i] * 9),
     "miaie_mlp_i8": (_i, [_p, _p, _p, _p, _p, _p] + [_i] * 6),
     "miaie_fill_i8": (_i, [_p, _p, _sz, _u64]),
+    "miaie_plan_gemm_i8": (_i, [_p, _i, _i, _i, _p]),
     "miaie_graph_begin": (_i, [_p]),
     "miaie_graph_end": (_i, [_p, C.POINTER(_p)]),
     "miaie_graph_launch": (_i, [_p, _p]),
@@ -132,6 +133,19 @@ def _addr(x) -> int | None:
     if isinstance(x, DeviceBuffer):
         return x.ptr
     return int(x)
+
+
+KERNEL_TILE64 = 0
+KERNEL_PIPE = 1
+
+
+class GemmPlan(C.Structure):
+    """miaie_gemm_plan (include/miaie.h)."""
+    _fields_ = [("kernel", C.c_int), ("tile_m", C.c_int), ("tile_n", C.c_int), ("workgroups", C.c_int),
+                ("threads", C.c_int)]
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
 
 
 class Graph:
@@ -262,6 +276,11 @@ class Context:
 
     def fill_i8(self, buf, n: int, tensor_id: int) -> None:
         self._call("miaie_fill_i8", _addr(buf), _sz(n), _u64(tensor_id))
+
+    def plan_gemm_i8(self, M: int, N: int, K: int) -> dict:
+        plan = GemmPlan()
+        self._call("miaie_plan_gemm_i8", M, N, K, C.addressof(plan))
+        return plan.as_dict()
 
     def record(self) -> _Recording:
         """`with ctx.record() as g: <entry points>` records them into g

@@ -84,18 +84,29 @@ __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + (
 //      of one column per lane) are read with two ds_read_b64_tr_b8, which
 //      transpose 8x16 byte blocks on the fly; bswz spreads the 8 k-rows x 2
 //      column halves one 32-lane half reads over all banks.
-constexpr int BM = 256, BK = 64, STAGES = 4;
+constexpr int BK = 64, STAGES = 4;
 
-template <int BN>
+// NW waves (4 or 8) tile the BM x BN workgroup tile as 2 x (NW/2): each
+// wave owns WM = BM/2 rows (NI = WM/32 A fragments) and WN = BN / (NW/2)
+// columns (NJ = WN/32 B fragments).
+template <int BM, int BN, int NW>
 struct PipeGeom {
-  static constexpr int A_BYTES = BM * BK;             // 16 KiB
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int WAVES_N = NW / 2;
+  static constexpr int WM = BM / 2;                    // rows per wave
+  static constexpr int WN = BN / WAVES_N;              // columns per wave
+  static constexpr int NI = WM / 32;                   // A fragments per wave per k-step
+  static constexpr int A_BYTES = BM * BK;             // 16 or 8 KiB
   static constexpr int B_BYTES = BN * BK;             // 16 or 8 KiB
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
-  static constexpr int B_CP = B_BYTES / 4096;          // B copies per thread per tile (4 or 2)
-  static constexpr int CP_PER_TILE = 4 + B_CP;         // 16-byte LDS copies per thread per tile
-  static constexpr int NJ = BN / 64;                   // B fragments per wave per k-step
-  static constexpr int NMF = 4 * NJ;                   // MFMAs per wave per k-step
+  static constexpr int CP_BYTES = 1024 * NW;          // one 16-byte copy by every thread
+  static constexpr int A_CP = A_BYTES / CP_BYTES;     // A copies per thread per tile
+  static constexpr int B_CP = B_BYTES / CP_BYTES;     // B copies per thread per tile
+  static constexpr int CP_PER_TILE = A_CP + B_CP;     // 16-byte LDS copies per thread per tile
+  static constexpr int NJ = WN / 32;                   // B fragments per wave per k-step
+  static constexpr int NMF = NI * NJ;                  // MFMAs per wave per k-step
+  static_assert(NI >= 1 && NJ >= 1 && A_CP >= 1 && B_CP >= 1, "tile too small for this many waves");
   static_assert(BM * BN <= LDS_BYTES, "Y staging fits in the stages");
 };
 
@@ -104,12 +115,12 @@ __device__ __forceinline__ int bswz(int k) {
   return BN == 256 ? (k & 7) << 1 : ((k >> 1) & 3) << 1;
 }
 
-template <int BN, bool B_NT, bool WRITE_Y, bool WRITE_C>
-__global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
+template <int BM, int BN, int NW, bool B_NT, bool WRITE_Y, bool WRITE_C>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
     int relu) {
-  using G = PipeGeom<BN>;
+  using G = PipeGeom<BM, BN, NW>;
   __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS_BYTES];
   const uint32_t lds0 = dev::lds_addr(lds);
 
@@ -120,18 +131,19 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
   int tm, tn;
   dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  const int KT = K / BK;
 
-  // ---- LDS copy assignment.  Copy i of wave w fills the 1 KiB block 4i + w
+  // ---- LDS copy assignment.  Copy i of wave w fills the 1 KiB block NW*i + w
   // of an operand's stage region:
-  //   A (and NT B): rows 64i + 16w + lane/4, physical chunk lane%4;
-  //   NN B: k-rows (4i + w) * (1024 / BN) + lane / (BN / 16), physical chunk
-  //   lane % (BN / 16).
+  //   A (and NT B): rows 16*(NW*i + w) + lane/4, physical chunk lane%4;
+  //   NN B: k-rows (NW*i + w) * (1024 / BN) + lane / (BN / 16), physical
+  //   chunk lane % (BN / 16).
   const int a_r = 16 * wave + (lane >> 2);
-  const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 3) ^ swz(a_r));  // swz(a_r + 64i) == swz(a_r)
+  const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 3) ^ swz(a_r));  // swz(a_r + 16*NW*i) == swz(a_r)
   const int8_t* const a_base = A + (size_t)m0 * lda;
   uint32_t b_voff;
   const int8_t* b_base;
-  constexpr int B_ROWS_PER_CP = B_NT ? 64 : 4096 / BN;  // operand rows between copies i and i+1
+  constexpr int B_ROWS_PER_CP = B_NT ? 16 * NW : 1024 * NW / BN;  // operand rows between copies i and i+1
   if constexpr (B_NT) {
     b_voff = (uint32_t)a_r * ldb + 16 * ((lane & 3) ^ swz(a_r));
     b_base = B + (size_t)n0 * ldb;
@@ -145,57 +157,57 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
   // copy x (< CP_PER_TILE) of tile kt into stage `stage`
   auto copy = [&](int kt, int stage, int x) {
     const uint32_t st = lds0 + stage * G::STAGE_BYTES + 1024 * wave;
-    if (x < 4) {
-      dev::gload_lds16(a_base + (size_t)kt * BK + (size_t)(64 * x) * lda, a_voff, st + 4096 * x);
+    if (x < G::A_CP) {
+      dev::gload_lds16(a_base + (size_t)kt * BK + (size_t)(16 * NW * x) * lda, a_voff, st + G::CP_BYTES * x);
     } else {
-      const int i = x - 4;
+      const int i = x - G::A_CP;
       const int8_t* bb = B_NT ? b_base + (size_t)kt * BK : b_base + (size_t)kt * BK * ldb;
-      dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * i) * ldb, b_voff, st + G::A_BYTES + 4096 * i);
+      dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * i) * ldb, b_voff, st + G::A_BYTES + G::CP_BYTES * i);
     }
   };
 
   // ---- fragment offsets within a stage.
   // A fragment (ks, i): row wm*128 + 32i + lane%32, logical chunk 2ks + lane/32.
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
   const int fr = lane & 31, fh = lane >> 5;
-  int a_fo[2], b_fo[4];
+  int a_fo[2], b_fo[G::NJ > 2 ? G::NJ : 2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) a_fo[ks] = (wm * 128 + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+  for (int ks = 0; ks < 2; ++ks) a_fo[ks] = (wm * G::WM + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
   if constexpr (B_NT) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      b_fo[ks] = G::A_BYTES + (wn * (BN / 2) + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+      b_fo[ks] = G::A_BYTES + (wn * G::WN + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
   } else {
     // tr8 read (ks, j, r): lane 16g + 2jj + h supplies k-row 32ks + 16(g>>1) + 8r + jj,
-    // columns wn*BN/2 + 32j + 16(g&1) + 8h .. +8; it receives column
-    // wn*BN/2 + 32j + lane%32, k = 32ks + 16*(lane/32) + 8r + (0..7).
+    // columns wn*WN + 32j + 16(g&1) + 8h .. +8; it receives column
+    // wn*WN + 32j + lane%32, k = 32ks + 16*(lane/32) + 8r + (0..7).
     // bswz of those k-rows depends on jj only.
     const int g = lane >> 4, jj = (lane >> 1) & 7, h = lane & 1;
 #pragma unroll
     for (int j = 0; j < G::NJ; ++j) {
-      const int c = wn * (BN / 32) + 2 * j + (g & 1);
+      const int c = wn * (G::WN / 16) + 2 * j + (g & 1);
       b_fo[j] = G::A_BYTES + (16 * (g >> 1) + jj) * BN + ((c ^ bswz<BN>(jj)) << 4) + 8 * h;
     }
   }
 
-  // One k-step's fragments: 4 A fragments, and NJ B fragments (NT: one
+  // One k-step's fragments: NI A fragments, and NJ B fragments (NT: one
   // ds_read_b128 each; NN: two tr8 halves each).
   struct Frags {
-    v4i a[4];
+    v4i a[G::NI];
     v4i b[G::NJ];                  // NT
     miaie_v2i lo[G::NJ], hi[G::NJ];  // NN
   };
-  constexpr int NREAD = 4 + (B_NT ? 1 : 2) * G::NJ;  // LDS read instructions per k-step
+  constexpr int NREAD = G::NI + (B_NT ? 1 : 2) * G::NJ;  // LDS read instructions per k-step
   // q-th LDS read of k-step ks of `stage` into f
   auto read_one = [&](int stage, int ks, int q, Frags& f) {
     const int8_t* s = lds + stage * G::STAGE_BYTES;
-    if (q < 4) {
+    if (q < G::NI) {
       f.a[q] = *reinterpret_cast<const v4i*>(s + a_fo[ks] + 2048 * q);
     } else if constexpr (B_NT) {
-      f.b[q - 4] = *reinterpret_cast<const v4i*>(s + b_fo[ks] + 2048 * (q - 4));
+      f.b[q - G::NI] = *reinterpret_cast<const v4i*>(s + b_fo[ks] + 2048 * (q - G::NI));
     } else {
-      const int j = (q - 4) >> 1;
-      if ((q & 1) == 0)
+      const int j = (q - G::NI) >> 1;
+      if (((q - G::NI) & 1) == 0)
         f.lo[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN);
       else
         f.hi[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN + 8 * BN);
@@ -212,14 +224,13 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
   // the rounding term 2^(shift-1) so the epilogue needs no add.
   const int rnd = shift ? 1 << (shift - 1) : 0;
   const int acc0 = (WRITE_Y && !WRITE_C) ? rnd : 0;
-  v16i acc[4][G::NJ];
+  v16i acc[G::NI][G::NJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < G::NI; ++i)
 #pragma unroll
     for (int j = 0; j < G::NJ; ++j)
       acc[i][j] = v16i{acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0};
 
-  const int KT = K / BK;
   constexpr int CP = G::CP_PER_TILE;
   // ---- prologue: tiles 0..3 in flight, wait for tile 0
 #pragma unroll
@@ -302,17 +313,17 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
   if (kt == KT - 2) tile(kt++, F_{}, T_{}, V0{});
   tile(kt, F_{}, F_{}, V0{});
 
-  // ---- epilogue.  acc[i][j][4g + t]: row m = wm*128 + 32i + lane%32,
-  // column n = wn*BN/2 + 32j + 8g + 4*(lane/32) + t.
+  // ---- epilogue.  acc[i][j][4g + t]: row m = wm*WM + 32i + lane%32,
+  // column n = wn*WN + 32j + 8g + 4*(lane/32) + t.
   if constexpr (WRITE_C) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::NI; ++i)
 #pragma unroll
       for (int j = 0; j < G::NJ; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int m = m0 + wm * 128 + 32 * i + fr;
-          const int n = n0 + wn * (BN / 2) + 32 * j + 8 * g + 4 * fh;
+          const int m = m0 + wm * G::WM + 32 * i + fr;
+          const int n = n0 + wn * G::WN + 32 * j + 8 * g + 4 * fh;
           v4i v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
           *reinterpret_cast<v4i*>(C + (size_t)m * ldc + n) = v;
         }
@@ -326,13 +337,13 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
     const Requant rq{shift, rnd - acc0, relu ? 0 : -128, 127};
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::NI; ++i)
 #pragma unroll
       for (int j = 0; j < G::NJ; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int m = wm * 128 + 32 * i + fr;
-          const int n = wn * (BN / 2) + 32 * j + 8 * g + 4 * fh;
+          const int m = wm * G::WM + 32 * i + fr;
+          const int n = wn * G::WN + 32 * j + 8 * g + 4 * fh;
           const uint32_t packed = rq.pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                                            acc[i][j][4 * g + 3]);
           const int off = m * BN + ((((n >> 4) ^ (m & (CH - 1)))) << 4) + (n & 15);
@@ -340,8 +351,8 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe(
         }
     __syncthreads();
 #pragma unroll
-    for (int it = 0; it < BM * CH / 256; ++it) {
-      const int flat = it * 256 + tid;
+    for (int it = 0; it < BM * CH / G::THREADS; ++it) {
+      const int flat = it * G::THREADS + tid;
       const int m = flat / CH, c = flat % CH;
       const v4i v = *reinterpret_cast<const v4i*>(lds + m * BN + ((c ^ (m & (CH - 1))) << 4));
       *reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + c * 16) = v;
@@ -436,56 +447,105 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64(const int8_t* __restrict__
   }
 }
 
-template <int BN, bool B_NT>
+template <int BM, int BN, bool B_NT>
 void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
                  int lda, int ldb, int ldy, int ldc, int shift, int relu) {
-  dim3 grid((M / BM) * (N / BN)), block(256);
+  constexpr int NW = 4;
+  dim3 grid((M / BM) * (N / BN)), block(64 * NW);
   if (Y && C)
-    hipLaunchKernelGGL((gemm_i8_pipe<BN, B_NT, true, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb,
-                       ldy, ldc, shift, relu);
+    hipLaunchKernelGGL((gemm_i8_pipe<BM, BN, NW, B_NT, true, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda,
+                       ldb, ldy, ldc, shift, relu);
   else if (Y)
-    hipLaunchKernelGGL((gemm_i8_pipe<BN, B_NT, true, false>), grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb,
-                       ldy, ldc, shift, relu);
+    hipLaunchKernelGGL((gemm_i8_pipe<BM, BN, NW, B_NT, true, false>), grid, block, 0, st, A, B, Y, C, M, N, K, lda,
+                       ldb, ldy, ldc, shift, relu);
   else
-    hipLaunchKernelGGL((gemm_i8_pipe<BN, B_NT, false, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb,
-                       ldy, ldc, shift, relu);
+    hipLaunchKernelGGL((gemm_i8_pipe<BM, BN, NW, B_NT, false, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda,
+                       ldb, ldy, ldc, shift, relu);
 }
 
-// Tile width for the pipelined kernel: 256 unless 128-wide tiles finish the
-// grid in fewer rounds of workgroups (one per CU), counting a 128-wide tile
-// as 0.55 of a 256-wide one.  0: neither fits the shape.
-int pick_bn(int M, int N, int cus) {
-  if (M % BM != 0) return 0;
-  const long rounds256 = N % 256 == 0 ? ((long)(M / BM) * (N / 256) + cus - 1) / cus : -1;
-  const long rounds128 = N % 128 == 0 ? ((long)(M / BM) * (N / 128) + cus - 1) / cus : -1;
-  if (rounds256 < 0) return rounds128 < 0 ? 0 : 128;
-  if (rounds128 < 0) return 256;
-  return rounds128 * 55 < rounds256 * 100 ? 128 : 256;
+// Tiling planner for the pipelined kernel: picks the workgroup tile
+// (BM x BN) among 256x256, 256x128 and 128x128 for an M x N x K product on
+// `cus` compute units.  Cost, in units of one 256x256x64 k-tile of MFMA
+// work: the rounds of one workgroup per CU times one workgroup's work, its
+// K/64 k-tiles plus about 6 units of prologue and epilogue, scaled by the
+// tile's relative cost per k-tile (1 for 256x256; 0.55 for 256x128; 0.35
+// for 128x128, whose LDS reads per MFMA are twice those of 256x256).
+struct TileChoice {
+  int bm, bn;
+  double unit;
+};
+constexpr TileChoice kTiles[] = {{256, 256, 1.0}, {256, 128, 0.55}, {128, 128, 0.35}};
+
+struct PipePlan {
+  int bm = 0, bn = 0;
+};
+
+PipePlan plan_pipe(int M, int N, int K, int cus) {
+  PipePlan best;
+  if (K % BK != 0 || cus < 1) return best;
+  double best_cost = 0;
+  for (const TileChoice& t : kTiles) {
+    if (M % t.bm != 0 || N % t.bn != 0) continue;
+    const long tiles = (long)(M / t.bm) * (N / t.bn);
+    const double cost = (double)((tiles + cus - 1) / cus) * t.unit * (K / BK + 6.0);
+    if (best.bm == 0 || cost < best_cost - 1e-9) {
+      best_cost = cost;
+      best.bm = t.bm;
+      best.bn = t.bn;
+    }
+  }
+  return best;
 }
 
 }  // namespace
 
 namespace miaie {
 
+// The pipelined kernel's operand conditions: 16-byte chunks (16-byte
+// aligned operands and strides), per-lane offsets of up to 64 rows in 32
+// bits, and the requant shortcut's K < 2^16.
+static bool pipe_operands_ok(const int8_t* A, const int8_t* B, const int8_t* Y, const int32_t* C, int K, int lda,
+                             int ldb, int ldy, int ldc) {
+  return (K % BK == 0) && (!Y || K < (1 << 16)) && aligned(A, 16) && aligned(B, 16) && lda % 16 == 0 &&
+         ldb % 16 == 0 && lda < (1 << 25) && ldb < (1 << 25) && (!Y || (aligned(Y, 16) && ldy % 16 == 0)) &&
+         (!C || (aligned(C, 16) && ldc % 4 == 0));
+}
+
+int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_plan* plan) {
+  const PipePlan p = dense_ok ? plan_pipe(M, N, K, ctx->cus) : PipePlan{};
+  *plan = miaie_gemm_plan{};
+  plan->threads = 256;
+  if (p.bm) {
+    plan->kernel = MIAIE_KERNEL_PIPE;
+    plan->tile_m = p.bm;
+    plan->tile_n = p.bn;
+    plan->workgroups = (M / p.bm) * (N / p.bn);
+  } else {
+    plan->kernel = MIAIE_KERNEL_TILE64;
+    plan->tile_m = 64;
+    plan->tile_n = 64;
+    plan->workgroups = ((M + 63) / 64) * ((N + 63) / 64);
+  }
+  return MIAIE_OK;
+}
+
 // Chooses the kernel.  Y and/or C may be NULL (not both).
 int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
                    int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu) {
-  // The 256x256 kernel copies 16-byte chunks (16-byte aligned operands and
-  // strides), keeps per-lane offsets of up to 64 rows in 32 bits, and its
-  // requant shortcut needs K < 2^16.
-  const int bn = pick_bn(M, N, ctx->cus);
-  const bool big = bn != 0 && (K % BK == 0) && (!Y || K < (1 << 16)) && aligned(A, 16) &&
-                   aligned(B, 16) && lda % 16 == 0 && ldb % 16 == 0 && lda < (1 << 25) && ldb < (1 << 25) &&
-                   (!Y || (aligned(Y, 16) && ldy % 16 == 0)) && (!C || (aligned(C, 16) && ldc % 4 == 0));
-  if (big) {
-    if (bn == 256 && b_nt)
-      launch_pipe<256, true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
-    else if (bn == 256)
-      launch_pipe<256, false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
-    else if (b_nt)
-      launch_pipe<128, true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+  miaie_gemm_plan plan;
+  plan_gemm_i8(ctx, M, N, K, pipe_operands_ok(A, B, Y, C, K, lda, ldb, ldy, ldc), &plan);
+  if (plan.kernel == MIAIE_KERNEL_PIPE) {
+    hipStream_t st = ctx->stream;
+    const int bm = plan.tile_m, bn = plan.tile_n;
+    if (bm == 256 && bn == 256)
+      b_nt ? launch_pipe<256, 256, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu)
+           : launch_pipe<256, 256, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+    else if (bm == 256)
+      b_nt ? launch_pipe<256, 128, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu)
+           : launch_pipe<256, 128, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
     else
-      launch_pipe<128, false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+      b_nt ? launch_pipe<128, 128, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu)
+           : launch_pipe<128, 128, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
     return check_launch(ctx, "gemm_i8_pipe");
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64), block(256);

@@ -42,6 +42,9 @@ __host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (re
 // ---- kernel launchers implemented in the kernel translation units ----
 int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
                    int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu);
+// Kernel plan for dense operands (dense_ok: the pipelined kernel's operand
+// conditions hold).
+int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_plan* plan);
 int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float* C, int M, int N,
                      int K);
 int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts,

@@ -305,6 +305,15 @@ extern "C" int miaie_fill_i8(miaie_ctx* ctx, int8_t* dst, size_t n, uint64_t ten
 
 extern "C" const char* miaie_version(void) { return "miaie 0.1 (gfx950)"; }
 
+// ---------------------------------------------------------------- GEMM plan
+extern "C" int miaie_plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, miaie_gemm_plan* plan) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  MIAIE_CHECK_NOT_NULL(ctx, plan);
+  if (M < 1 || N < 1 || K < 1) return fail(ctx, MIAIE_EINVAL, "miaie_plan_gemm_i8: M=%d N=%d K=%d", M, N, K);
+  return plan_gemm_i8(ctx, M, N, K, (K % 16 == 0) && (N % 16 == 0) && K < (1 << 16), plan);
+}
+
 // ---------------------------------------------------------------- recorded chains
 struct miaie_graph {
   int device = 0;

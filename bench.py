@@ -11,6 +11,8 @@ Also in the line (not the headline):
   extras.conv2d_3x3      int8 3x3 conv2d, N=8 56x56 Cin=Cout=64 (GOPS, roofline)
   extras.gemm_bf16_8192  bf16 8192^3 GEMM, fp32 accumulate/output (TFLOP/s)
   extras.mlp_i8          chained int8 MLP 2048x4096 -> 11008 -> 4096 (TOP/s)
+  extras.gemm_i8_m_shard one GPU's 512- and 256-row share of the 4096^3 GEMM
+                         sharded over M, with the tile the planner picks
   extras.mfma_ceiling    register-only MFMA rate on this GPU, constant and
                          random operands (aiehlc_amd/probes/mfma_ceiling)
   extras.vendor_library  the same int8 4096^3 and bf16 8192^3 products through
@@ -279,6 +281,22 @@ def main() -> int:
         }
         for b in (dX, dW, dS, dYc):
             b.free()
+        # one GPU's share of the 4096^3 GEMM sharded 8 and 16 ways over M: the
+        # planner picks 128x128 tiles so the grid still covers the CUs
+        shard = {}
+        for Ms in (512, 256):
+            dAs, dBs, dYs = ctx.empty((Ms, K), np.int8), ctx.empty((K, N), np.int8), ctx.empty((Ms, N), np.int8)
+            ctx.fill_i8(dAs, Ms * K, 1)
+            ctx.fill_i8(dBs, K * N, 2)
+            ms_s = timed(ctx, timer, lambda: ctx.gemm_i8_rq(dAs, dBs, dYs, Ms, N, K, 10, False, None, mi.B_NN),
+                         args.steps, args.warmup)
+            sops = 2.0 * Ms * N * K
+            shard[f"M{Ms}"] = {"shape": [Ms, N, K], "plan": ctx.plan_gemm_i8(Ms, N, K), "us": round(ms_s * 1e3, 2),
+                               "tops": round(sops / (ms_s * 1e-3) / 1e12, 1),
+                               "frac_of_peak": round(sops / (ms_s * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+            for b in (dAs, dBs, dYs):
+                b.free()
+        extras["gemm_i8_m_shard"] = shard
         # config 3: bf16 8192^3
         Mb = 8192
         dAb, dBb, dCb = (ctx.empty((Mb, Mb), np.uint16), ctx.empty((Mb, Mb), np.uint16),

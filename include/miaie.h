@@ -92,6 +92,23 @@ MIAIE_API int miaie_copy_d2d(miaie_ctx* ctx, void* dst_dev, const void* src_dev,
  * (timeout_ms < 0 waits without a deadline). */
 MIAIE_API int miaie_wait(miaie_ctx* ctx, int timeout_ms);
 
+/* ---- GEMM planning ------------------------------------------------------ */
+
+#define MIAIE_KERNEL_TILE64 0 /* bounds-checked 64x64 kernel, any shape and stride */
+#define MIAIE_KERNEL_PIPE 1   /* pipelined tile_m x tile_n kernel, 4-stage LDS DMA pipeline */
+
+/* How miaie_gemm_i8_* would run an M x N x K product on this context with
+ * dense 16-byte-aligned operands (the tiling planner: the grid
+ * decomposition and tile choice that stand in for the reference's tiling
+ * prototype, src/mlir/mlirfront/tilinglinalg/tilinglinalg.cpp:38-146). */
+typedef struct {
+  int kernel;         /* MIAIE_KERNEL_* */
+  int tile_m, tile_n; /* workgroup output tile */
+  int workgroups;     /* grid size */
+  int threads;        /* per workgroup */
+} miaie_gemm_plan;
+MIAIE_API int miaie_plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, miaie_gemm_plan* plan);
+
 /* ---- recorded kernel chains --------------------------------------------- */
 
 /* The reference chains kernels through the host: run k1, wait, move k1's

@@ -1,0 +1,66 @@
+"""The tiling planner (miaie_plan_gemm_i8) and the tiles it picks.
+
+The planner chooses the pipelined kernel's workgroup tile (256x256,
+256x128 or 128x128) from the shape and the device's CU count; every choice
+must give the oracle's bits exactly, in every output mode and both B
+layouts.  Small-M products (one GPU's share of a GEMM sharded over M) are
+where the 128x128 tile is chosen."""
+import numpy as np
+import pytest
+
+import aiehlc_amd as mi
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def test_planner_choices(ctx):
+    full = ctx.plan_gemm_i8(4096, 4096, 4096)
+    assert (full["kernel"], full["tile_m"], full["tile_n"]) == (mi.KERNEL_PIPE, 256, 256)
+    assert full["workgroups"] == 256 and full["threads"] == 256
+    # one GPU's 512-row share of the 4096^3 GEMM: more, smaller tiles
+    shard = ctx.plan_gemm_i8(512, 4096, 4096)
+    assert (shard["tile_m"], shard["tile_n"], shard["workgroups"]) == (128, 128, 128)
+    # the MLP's projections keep 256-row tiles
+    assert (ctx.plan_gemm_i8(2048, 11008, 4096)["tile_m"], ctx.plan_gemm_i8(2048, 11008, 4096)["tile_n"]) == (256, 128)
+    assert ctx.plan_gemm_i8(2048, 4096, 11008)["tile_m"] == 256
+    # shapes the pipelined kernel cannot take
+    assert ctx.plan_gemm_i8(100, 50, 30)["kernel"] == mi.KERNEL_TILE64
+    assert ctx.plan_gemm_i8(128, 128, 100)["kernel"] == mi.KERNEL_TILE64
+    assert ctx.call_status("miaie_plan_gemm_i8", 0, 1, 1, None) == mi.MIAIE_EINVAL
+
+
+SHAPES = [(512, 4096, 4096, mi.B_NN), (256, 1024, 2048, mi.B_NT), (128, 2048, 1024, mi.B_NN),
+          (384, 640, 512, mi.B_NT), (128, 128, 64, mi.B_NN)]
+
+
+@pytest.mark.parametrize("M,N,K,layout", SHAPES)
+def test_128_tiles_match_the_oracle(ctx, M, N, K, layout):
+    plan = ctx.plan_gemm_i8(M, N, K)
+    print(f"[case] gemm {M}x{N}x{K} layout {layout} plan {plan}", flush=True)
+    assert (plan["tile_m"], plan["tile_n"]) == (128, 128)
+    rng = np.random.default_rng(M + N + K + layout)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(N, K) if layout == mi.B_NT else (K, N), dtype=np.int8)
+    dA, dB = ctx.upload(A), ctx.upload(B)
+    dC, dY, dY2, dC2 = (ctx.empty((M, N), np.int32), ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int8),
+                        ctx.empty((M, N), np.int32))
+    ctx.gemm_i8_i32(dA, dB, dC, M, N, K, b_layout=layout)          # C only
+    ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, layout)    # Y only
+    ctx.gemm_i8_rq(dA, dB, dY2, M, N, K, 11, True, dC2, layout)     # Y + C, ReLU
+    ctx.wait(60_000)
+    C = ctx.download(dC)
+    slabs = [(0, M)] if M * N * K <= 2**31 else [(0, 64), (M - 64, M)]
+    for r0, r1 in slabs:
+        assert np.array_equal(C[r0:r1], oracle.gemm_i8(A, B, b_nt=layout == mi.B_NT, rows=(r0, r1)))
+    assert np.array_equal(ctx.download(dY), oracle.requant(C, 10))
+    assert np.array_equal(ctx.download(dY2), oracle.requant(C, 11, relu=True))
+    assert np.array_equal(ctx.download(dC2), C)
+    if len(slabs) > 1:  # full-size check by linearity in A: C(2A') = 2 C(A')
+        A2 = (A // 2).astype(np.int8)
+        dA2 = ctx.upload((2 * A2.astype(np.int16)).astype(np.int8))
+        dAh, dCh = ctx.upload(A2), ctx.empty((M, N), np.int32)
+        ctx.gemm_i8_i32(dA2, dB, dC, M, N, K, b_layout=layout)
+        ctx.gemm_i8_i32(dAh, dB, dCh, M, N, K, b_layout=layout)
+        ctx.wait(60_000)
+        assert np.array_equal(ctx.download(dC), 2 * ctx.download(dCh))
