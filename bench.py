@@ -319,7 +319,7 @@ def main() -> int:
         ms_m = timed(ctx, timer, lambda: ctx.mlp_i8(dXm, d1, d2, dH, dYm, Mm, Km, Fm, Nm, 11, 12),
                      max(5, args.steps // 2), 2)
         mops = 2.0 * 2 * Mm * Km * Fm
-        extras["mlp_i8"] = {"kernel": "gemm_i8_pipe<128> x 2", "ms_per_step": round(ms_m, 4),
+        extras["mlp_i8"] = {"kernel": "gemm_i8_pipe<256, 128, 4, NN, Y> x 2", "ms_per_step": round(ms_m, 4),
                             "tops": round(mops / (ms_m * 1e-3) / 1e12, 1),
                             "frac_of_peak": round(mops / (ms_m * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
         for b in (dXm, d1, d2, dH, dYm):
@@ -331,7 +331,7 @@ def main() -> int:
 
     roofline = {
         "bound": "mfma",
-        "kernel": "gemm_i8_pipe<256, NN, Y>",
+        "kernel": "gemm_i8_pipe<256, 256, 4, NN, Y>",
         "achieved": round(tops, 2),
         "peak": PEAK_INT8_TOPS,
         "unit": "TFLOP/s",
