@@ -4,7 +4,8 @@ Compiles every aiehlc_amd/csrc/*.hip translation unit with hipcc for gfx950
 and links them into aiehlc_amd/lib/libmiaie.so, builds the aie-rt-shaped
 facade aiehlc_amd/csrc/xaie/*.hip into aiehlc_amd/lib/libmiaie_xaie.so on top
 of it, then the harness programs in aiehlc_amd/harness/ (C++ against
-miaie.hpp, C against miaie_xaie.h) and the measurement probes in
+miaie.hpp, C against miaie_xaie.h, and the aiehlc-dialect samples in
+harness/hlc/ through the hlc.py front end) and the measurement probes in
 aiehlc_amd/probes/.  Runs on a machine without a GPU
 (hipcc cross-compiles).
 
@@ -72,6 +73,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     os.replace(tmp, LIB)
     build_xaie(verbose)
     build_harness(verbose)
+    build_hlc_samples(verbose)
     build_probes(verbose)
     return LIB
 
@@ -108,6 +110,29 @@ def build_harness(verbose: bool = False) -> None:
         else:
             continue
         _run(cmd, verbose)
+        os.replace(exe + ".tmp", exe)
+
+
+def build_hlc_samples(verbose: bool = False) -> None:
+    """Programs in the aiehlc dialect (aiehlc_amd/harness/hlc/*.cc), rewritten
+    by aiehlc_amd/hlc.py and compiled with g++ into aiehlc_amd/harness/hlc_<name>."""
+    sdir = os.path.join(HARNESS, "hlc")
+    if not os.path.isdir(sdir):
+        return
+    sys.path.insert(0, ROOT)
+    from aiehlc_amd import hlc  # noqa: E402  (the front end is part of the package)
+    os.makedirs(OBJ, exist_ok=True)
+    for f in sorted(os.listdir(sdir)):
+        if not f.endswith(".cc"):
+            continue
+        src = os.path.join(sdir, f)
+        out, _, _ = hlc.rewrite(open(src).read(), filename=src)
+        host = os.path.join(OBJ, "hlc_" + f)
+        with open(host, "w") as fh:
+            fh.write(out)
+        exe = os.path.join(HARNESS, "hlc_" + f[:-3])
+        _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}", host, "-o",
+              exe + ".tmp", f"-L{LIBDIR}", "-lmiaie_xaie", "-lmiaie", "-Wl,-rpath,$ORIGIN/../lib"], verbose)
         os.replace(exe + ".tmp", exe)
 
 

@@ -32,7 +32,7 @@ constexpr u32 kMemTileMem = 512u << 10;   // memory tile
 constexpr u32 kMaxRunTiles = 500;         // tiles in one launch (kernel argument block)
 constexpr u32 kDefaultWaitUs = 500;
 
-enum Builtin : u32 { B_NONE = 0, B_MM_NT = 1, B_K1 = 2, B_K2 = 3, B_MM3_U64 = 4 };
+enum Builtin : u32 { B_NONE = 0, B_MM_NT = 1, B_K1 = 2, B_K2 = 3, B_MM3_U64 = 4, B_DOT_U8 = 5 };
 
 // ---------------------------------------------------------------- tile kernels
 struct TileList {
@@ -107,6 +107,8 @@ MIAIE_XAIE_API const XAie_MiaieKernel miaie_xaie_k2 = {
     MIAIE_XAIE_KERNEL_MAGIC, "k2", 2, {0, 0}, {0, 0}, 0, nullptr, nullptr, B_K2};
 MIAIE_XAIE_API const XAie_MiaieKernel miaie_xaie_mm3_u64 = {
     MIAIE_XAIE_KERNEL_MAGIC, "mm3_u64", 2, {0, 0}, {0, 0}, MIAIE_XAIE_KERNEL_FOREVER, nullptr, nullptr, B_MM3_U64};
+MIAIE_XAIE_API const XAie_MiaieKernel miaie_xaie_perf_u8 = {
+    MIAIE_XAIE_KERNEL_MAGIC, "perf_u8", 2, {0x1000, 0x6000}, {512, 512}, 0, nullptr, nullptr, B_DOT_U8};
 }
 
 namespace {
@@ -119,11 +121,13 @@ u32 builtin_extent(const XAie_MiaieKernel* k, u32 param, u32 arg) {
     case B_K1:
     case B_K2: return param == 0 ? 4 : 20 * 4;
     case B_MM3_U64: return param == 0 ? 9 * 8 : 10 * 8;
+    case B_DOT_U8: return param == 0 ? 4 : 5 * 4;
     default: return 0;
   }
 }
 
 thread_local std::string g_last_error;
+std::vector<miaie_xaie_dev*> g_devices;  // initialised instances, for XAie_MiaieRunOnDdr
 
 enum TileKind { T_NONE, T_SHIM, T_MEM, T_CORE };
 
@@ -290,7 +294,7 @@ AieRC valid_kernel(miaie_xaie_dev* d, const void* p, const XAie_MiaieKernel** ou
                 MIAIE_XAIE_MAX_PARAMS);
   if (k->Builtin == B_NONE && !k->Launch)
     return fail(d, XAIE_INVALID_ELF, "kernel %s: no launch function", k->Name ? k->Name : "?");
-  if (k->Builtin > B_MM3_U64) return fail(d, XAIE_INVALID_ELF, "kernel %s: unknown built-in", k->Name ? k->Name : "?");
+  if (k->Builtin > B_DOT_U8) return fail(d, XAIE_INVALID_ELF, "kernel %s: unknown built-in", k->Name ? k->Name : "?");
   if (k->Builtin != B_NONE && k->NumParams != 2)
     return fail(d, XAIE_INVALID_ELF, "built-in kernel %s must have 2 parameters", k->Name ? k->Name : "?");
   *out = k;
@@ -333,6 +337,15 @@ AieRC launch_group(miaie_xaie_dev* d, const XAie_MiaieKernel* k, u32 arg, const 
         break;
       case B_MM3_U64:
         tile_mm3_u64<<<tl.n, 64, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], passes);
+        break;
+      case B_DOT_U8:  // the whole-GPU MFMA probe of libmiaie, once per tile and pass
+        for (u32 i = 0; i < tl.n; ++i)
+          for (u32 p = 0; p < passes; ++p) {
+            uint8_t* base = d->mem + tl.off[i];
+            const int rc = miaie_dot_u8_probe(d->ctx, reinterpret_cast<const uint32_t*>(base + ping[0]),
+                                              reinterpret_cast<uint32_t*>(base + ping[1]));
+            if (rc) return miaie_fail(d, rc, "perf_u8");
+          }
         break;
     }
     hipError_t e = hipGetLastError();
@@ -424,6 +437,8 @@ void free_ddr(XAie_MemInst* m) {
 }
 
 void destroy(miaie_xaie_dev* d) {
+  for (size_t i = 0; i < g_devices.size(); ++i)
+    if (g_devices[i] == d) g_devices.erase(g_devices.begin() + (long)i--);
   if (d->ctx) miaie_wait(d->ctx, -1);
   for (auto& f : d->inflight) (void)hipEventDestroy(f.second);
   for (hipEvent_t e : d->spare) (void)hipEventDestroy(e);
@@ -558,6 +573,7 @@ MIAIE_XAIE_API AieRC XAie_CfgInitialize(XAie_DevInst* DevInst, const XAie_Config
   DevInst->Backend = &kBackends[0];
   DevInst->Priv = d;
   DevInst->IsReady = 1;
+  g_devices.push_back(d);
   return XAIE_OK;
 }
 
@@ -964,7 +980,8 @@ AieRC implicit_open() {
 }
 
 const XAie_MiaieKernel* builtin_by_name(const char* name) {
-  const XAie_MiaieKernel* all[] = {&miaie_xaie_mm, &miaie_xaie_perf, &miaie_xaie_k1, &miaie_xaie_k2, &miaie_xaie_mm3_u64};
+  const XAie_MiaieKernel* all[] = {&miaie_xaie_mm,  &miaie_xaie_perf,    &miaie_xaie_k1,
+                                   &miaie_xaie_k2,  &miaie_xaie_mm3_u64, &miaie_xaie_perf_u8};
   for (const XAie_MiaieKernel* k : all)
     if (strcmp(k->Name, name) == 0) return k;
   return nullptr;
@@ -1082,3 +1099,64 @@ MIAIE_XAIE_API AieRC XAie_KernelFree(XAie_Kernel_Inst* K) {
 }
 
 }  // extern "C"
+
+// ======================================================================== launches on DDR addresses
+extern "C" MIAIE_XAIE_API AieRC XAie_MiaieRunOnDdr(const XAie_MiaieKernel* Kernel, u32 Cols, u32 Rows, u32 ColStart,
+                                                   u32 RowStart, u64 InAddr, u64 OutAddr) {
+  const XAie_MiaieKernel* k = nullptr;
+  if (AieRC rc = valid_kernel(nullptr, Kernel, &k)) return rc;
+  if (k->NumParams != 2) return fail(nullptr, XAIE_NOT_SUPPORTED, "XAie_MiaieRunOnDdr: kernel %s has %u windows, not 2",
+                                     k->Name ? k->Name : "?", k->NumParams);
+  if (Cols == 0 || Rows == 0) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_MiaieRunOnDdr: %u x %u tiles", Cols, Rows);
+  // the instance whose XAie_MemAllocate buffers hold both addresses
+  miaie_xaie_dev* d = nullptr;
+  XAie_MemInst *min = nullptr, *mout = nullptr;
+  for (miaie_xaie_dev* c : g_devices) {
+    XAie_MemInst* a = find_ddr(c, (uintptr_t)InAddr, 1);
+    XAie_MemInst* b = find_ddr(c, (uintptr_t)OutAddr, 1);
+    if (a && b) {
+      d = c, min = a, mout = b;
+      break;
+    }
+  }
+  if (!d)
+    return fail(nullptr, XAIE_INVALID_ARGS,
+                "XAie_MiaieRunOnDdr: 0x%llx / 0x%llx are not both in XAie_MemAllocate buffers of one initialised instance",
+                (unsigned long long)InAddr, (unsigned long long)OutAddr);
+  if (hipSetDevice(d->device) != hipSuccess) return fail(d, XAIE_ERR, "XAie_MiaieRunOnDdr: hipSetDevice");
+  u32 ping[MIAIE_XAIE_MAX_PARAMS];
+  window_layout(k, ping, nullptr);
+  // bytes moved: the input window (as much of it as the buffer holds) and
+  // what the kernel writes (the output window of a user kernel)
+  const u32 win_in = 4 * 4 * (k->SizeHint[0] ? k->SizeHint[0] : 512);
+  const u32 in_bytes = (u32)std::min<uint64_t>(win_in, min->size - (InAddr - (uintptr_t)min->host));
+  const u32 out_bytes = k->Builtin ? builtin_extent(k, 1, 16) : 4 * 4 * (k->SizeHint[1] ? k->SizeHint[1] : 512);
+  const uint64_t out_room = mout->size - (OutAddr - (uintptr_t)mout->host);
+  if ((uint64_t)out_bytes * Cols * Rows > out_room)
+    return fail(d, XAIE_INVALID_ARGS, "XAie_MiaieRunOnDdr: %u tiles x %u B of output exceed the buffer (%llu B)",
+                Cols * Rows, out_bytes, (unsigned long long)out_room);
+  std::vector<int> tiles;
+  for (u32 c = 0; c < Cols; ++c)
+    for (u32 r = 0; r < Rows; ++r) {
+      const XAie_LocType loc = XAie_TileLoc((u8)(ColStart + c), (u8)(RowStart + r));
+      int t;
+      if (ColStart + c > 255 || RowStart + r > 255) return fail(d, XAIE_INVALID_TILE, "XAie_MiaieRunOnDdr: tile outside");
+      if (AieRC rc = core_of(d, loc, "XAie_MiaieRunOnDdr", &t)) return rc;
+      if (AieRC rc = check_windows(d, k, 16, d->bytes[t])) return rc;
+      tiles.push_back(t);
+    }
+  if (AieRC rc = flush(d)) return rc;
+  for (int t : tiles) {
+    if (AieRC rc = copy_h2d(d, t, ping[0], reinterpret_cast<const void*>((uintptr_t)InAddr), in_bytes)) return rc;
+    Core& c = d->cores[t];
+    c.k = k;
+    c.arg = 16;
+    c.reset = false;
+    c.enabled = true;
+  }
+  if (AieRC rc = launch_cores(d, tiles, 1)) return rc;
+  for (size_t i = 0; i < tiles.size(); ++i)
+    if (AieRC rc = copy_d2h(d, tiles[i], ping[1], reinterpret_cast<void*>((uintptr_t)OutAddr + i * out_bytes), out_bytes))
+      return rc;
+  return XAIE_OK;
+}

@@ -147,7 +147,11 @@ typedef struct {
   struct miaie_xaie_dev* Priv; /* facade state: device, tile memories, cores */
 } XAie_DevInst;
 
+#ifdef __cplusplus
+#define XAie_InstDeclare(Inst, ConfigPtr) XAie_DevInst Inst = {}
+#else
 #define XAie_InstDeclare(Inst, ConfigPtr) XAie_DevInst Inst = {0}
+#endif
 
 typedef struct XAie_MemInst XAie_MemInst;
 typedef struct XAie_RoutingInstance XAie_RoutingInstance;
@@ -192,6 +196,8 @@ MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_k1;     /* multi_tile.cp
 MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_k2;     /* multi_tile.cpp:44-47: out[0..20) = in[0] + 10 */
 MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_mm3_u64;/* vek385_verification.cpp:56-69: 3x3 A.A forever, counter at out[9] */
 
+MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_perf_u8;/* aie_nokernelload.cc:50-83: uint8 MAC probe, in[0] at 0x1000 -> 5 words at 0x6000 */
+
 /* Iterations a FOREVER kernel runs per XAie_CoreEnable: the GPU runs a
  * bounded grid, so "until disabled" becomes this many passes, and the pass
  * counter the kernel keeps (out[9] for mm3_u64) ends at this value. */
@@ -205,6 +211,18 @@ MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_mm3_u64;/* vek385_verifi
  * are 2i (ping) and 2i+1 (pong).  Fills ping[] and pong[] (NumParams entries
  * each; either may be NULL).  Pure host computation. */
 MIAIE_XAIE_API AieRC XAie_MiaieWindowLayout(const XAie_MiaieKernel* Kernel, u32* Ping, u32* Pong);
+
+/* Run a two-window kernel on the Cols x Rows tiles from (ColStart, RowStart)
+ * with DDR addresses as its arguments: the launch the reference's
+ * `__kernel__` template call stands for, perf<1,1,4,4,256,16,64>(phy, phy_out)
+ * (aie_nokernelload.cc:130), where phy / phy_out are XAie_MemGetDevAddr
+ * values.  Each tile gets the input window from InAddr (as much as the
+ * buffer holds); tile i's output (what the kernel writes) lands at
+ * OutAddr + i * that size.  The addresses must lie in XAie_MemAllocate
+ * buffers of one initialised instance; the tiles' cores are loaded with the
+ * kernel and run once.  Returns when the output is in DDR. */
+MIAIE_XAIE_API AieRC XAie_MiaieRunOnDdr(const XAie_MiaieKernel* Kernel, u32 Cols, u32 Rows, u32 ColStart, u32 RowStart,
+                                        u64 InAddr, u64 OutAddr);
 
 /* Text of the last failure on this instance ("" if none).  With a NULL or
  * uninitialised instance: the last failure of any instance on this thread. */
