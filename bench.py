@@ -129,6 +129,7 @@ def cpu_baseline(seconds: float) -> dict:
     tops1 = 2.0 * 16 * N * K / t1 / 1e12
     t_os = run(oracle._lib("liboracle_os.so"), 16, 1)
     tops_os = 2.0 * 16 * N * K / t_os / 1e12
+    others = other_cpu_goldens(threads)
     return {
         "value": round(tops, 6),
         "unit": "TOP/s",
@@ -142,7 +143,62 @@ def cpu_baseline(seconds: float) -> dict:
         "single_thread_Os_value": round(tops_os, 6),
         "single_thread_Os_sample": f"rows 0..16, 1 thread, gcc -Os (the reference host's flag, script/aiehlc.sh:343), "
                                    f"{t_os:.2f} s",
+        "host_cpu": host_cpu(),
+        "other_configs": others,
     }
+
+
+def host_cpu() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return f"{line.split(':', 1)[1].strip()} ({os.cpu_count()} logical CPUs visible)"
+    except OSError:
+        pass
+    return f"unknown ({os.cpu_count()} logical CPUs visible)"
+
+
+def other_cpu_goldens(threads: int) -> dict:
+    """The oracle's golden loops on the other configs (same seeded inputs as
+    the GPU side): config 1 (64^3, one thread), the conv in full, and
+    256-row slabs of the MLP and of the bf16 GEMM, extrapolated to the whole
+    output by row count (stated)."""
+    import oracle
+    from aiehlc_amd import synth
+
+    out = {}
+    A, B = synth.int8((64, 64), 1), synth.int8((64, 64), 2)
+    t0 = time.perf_counter()
+    for _ in range(100):
+        oracle.gemm_i8(A, B, nthreads=1)
+    t = (time.perf_counter() - t0) / 100
+    out["config1_gemm_64"] = {"seconds": round(t, 7), "gops": round(2.0 * 64**3 / t / 1e9, 3), "threads": 1}
+    X, W = synth.int8((8, 56, 56, 64), 3), synth.int8((64, 3, 3, 64), 4)
+    sh = synth.shifts(64, 7)
+    t0 = time.perf_counter()
+    oracle.conv2d_nhwc_i8(X, W, sh, nthreads=threads)
+    t = time.perf_counter() - t0
+    out["config4_conv2d"] = {"seconds": round(t, 4), "gops": round(2.0 * 8 * 56 * 56 * 64 * 64 * 9 / t / 1e9, 2),
+                             "threads": threads, "sample": "the whole output, direct 7-loop nest"}
+    # the generators are counter-based, so the first 256 rows of X (and of
+    # the bf16 A below) are generated alone
+    Xm, W1, W2 = synth.int8((256, 4096), 3), synth.int8((4096, 11008), 5), synth.int8((11008, 4096), 6)
+    t0 = time.perf_counter()
+    oracle.mlp_i8(Xm, W1, W2, 11, 12, rows=(0, 256), nthreads=threads)
+    t = time.perf_counter() - t0
+    out["config5_mlp"] = {"seconds_extrapolated": round(t * 2048 / 256, 3),
+                          "tops": round(2.0 * 2 * 256 * 4096 * 11008 / t / 1e12, 5), "threads": threads,
+                          "sample": f"rows 0..256 of 2048 in {t:.2f} s, extrapolated x8"}
+    del Xm, W1, W2
+    Ab = synth.bf16_normal((256, 8192), 1, 1.0 / np.sqrt(8192))
+    Bb = synth.bf16_normal((8192, 8192), 2, 1.0 / np.sqrt(8192))
+    t0 = time.perf_counter()
+    oracle.gemm_bf16(Ab, Bb, rows=(0, 256), nthreads=threads)
+    t = time.perf_counter() - t0
+    out["config3_gemm_bf16"] = {"seconds_extrapolated": round(t * 8192 / 256, 3),
+                                "tflops": round(2.0 * 256 * 8192 * 8192 / t / 1e12, 5), "threads": threads,
+                                "sample": f"rows 0..256 of 8192 (fp32 accumulate) in {t:.2f} s, extrapolated x32"}
+    return out
 
 
 def mfma_ceiling() -> dict | None:
