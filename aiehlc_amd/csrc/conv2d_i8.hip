@@ -264,8 +264,14 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
     for (int g = 0; g < 4; ++g) {
       uint32_t packed = 0;
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-        packed |= (uint32_t)(requant1(acc[4 * g + tt], (sh4[g] >> (8 * tt)) & 0xFF) & 0xFF) << (8 * tt);
+      for (int tt = 0; tt < 4; ++tt) {
+        // round half up, shift, saturate: |acc| <= 576 * 2^14, so adding
+        // 2^(s-1) cannot overflow for any s <= 31
+        const int sc = (sh4[g] >> (8 * tt)) & 0xFF;
+        const int rnd = (1 << sc) >> 1;
+        const int q = min(max((acc[4 * g + tt] + rnd) >> sc, -128), 127);
+        packed |= (uint32_t)(q & 0xFF) << (8 * tt);
+      }
       *reinterpret_cast<uint32_t*>(y + 8 * g) = packed;
     }
   }
