@@ -56,6 +56,28 @@ struct Requant {
   }
 };
 
+// The same requant for s >= 8 in 7 instructions per 4 values.  With
+// u = (acc + rnd) >> (s - 8), floor division composes, so u >> 8 equals
+// (acc + rnd) >> s, and the high byte of sat_int16(u) is that value clamped
+// to [-128, 127]: in range it is u >> 8; above 32767 it is 127 = 32767 >> 8
+// (and u >> 8 >= 128); below -32768 it is -128 (and u >> 8 <= -129).
+// v_cvt_pk_i16_i32 saturates two such u into one dword, v_perm_b32 collects
+// the four high bytes.  ReLU clamps the int16 pairs at 0 first.
+typedef short miaie_v2s __attribute__((ext_vector_type(2)));
+template <bool RELU>
+struct RequantHi {
+  int sh, rnd;  // sh = s - 8 (s >= 8)
+  __device__ __forceinline__ uint32_t pair(int a, int b) const {
+    miaie_v2s p = __builtin_amdgcn_cvt_pk_i16((a + rnd) >> sh, (b + rnd) >> sh);
+    if constexpr (RELU) p = __builtin_elementwise_max(p, miaie_v2s{0, 0});
+    return __builtin_bit_cast(uint32_t, p);
+  }
+  __device__ __forceinline__ uint32_t pack4(int a0, int a1, int a2, int a3) const {
+    // bytes 1 and 3 of pair(a0, a1), then bytes 1 and 3 of pair(a2, a3)
+    return __builtin_amdgcn_perm(pair(a2, a3), pair(a0, a1), 0x07050301u);
+  }
+};
+
 // LDS tile rows are 64 bytes = four 16-byte chunks; chunk c of row r is
 // stored at chunk c ^ swz(r).  gfx950 serves a ds_read_b128 16 lanes at a
 // time from 64 four-byte banks; the MFMA fragment read has lanes 0..15 on
@@ -66,10 +88,11 @@ __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + ((chunk ^ swz(row)) << 4); }
 
 // ---------------------------------------------------------- pipelined tile
-// Workgroup tile 256 x BN (BN = 256 or 128), k-step 64, four LDS stages.
-// The stages are the AIE DMA ping-pong generalised to depth 4: tile t+4 is
-// copied global -> LDS (global_load_lds_dwordx4, no register staging) while
-// tile t is multiplied, so each copy has three tiles of MFMA work to land.
+// Workgroup tile BM x BN (256x256, 256x128 or 128x128), k-step 64, four LDS
+// stages.  The stages are the AIE DMA ping-pong generalised to depth 4: tile
+// t+4 is copied global -> LDS (global_load_lds_dwordx4, no register staging)
+// while tiles t and t+1 are multiplied, half of it in each, so each copy has
+// over two tiles of MFMA work to land.
 // Each of the 4 waves owns a 128 x BN/2 quarter: 4 x (BN/64)
 // v_mfma_i32_32x32x32_i8 per 32-wide k-step, fragments double-buffered in
 // registers so the LDS reads of one k-step overlap the MFMAs of the other.
@@ -115,12 +138,41 @@ __device__ __forceinline__ int bswz(int k) {
   return BN == 256 ? (k & 7) << 1 : ((k >> 1) & 3) << 1;
 }
 
-template <int BM, int BN, int NW, bool B_NT, bool WRITE_Y, bool WRITE_C>
+// Issue order of one k-step's LDS reads.  Reads are numbered as in
+// read_one (A fragment i -> i; NT B fragment j -> NI + j; NN B fragment j ->
+// NI + 2j and NI + 2j + 1, its two transposing halves), and go out in the
+// order the i-major MFMA sequence (i, j) = (x / NJ, x % NJ) first needs them:
+// B0, A0, B1 .. B(NJ-1), A1 .. A(NI-1).  With reads issued RPS per MFMA slot
+// from the start of a phase, every fragment has landed several MFMAs before
+// the next phase consumes it, and the last read of a phase is far from the
+// wait that precedes the tile barrier.
+template <int NI, int NJ, bool B_NT>
+constexpr int read_order(int n) {
+  if (B_NT) {
+    if (n == 0) return NI;
+    if (n == 1) return 0;
+    if (n <= NJ) return NI + n - 1;
+    return n - NJ;
+  }
+  if (n < 2) return NI + n;
+  if (n == 2) return 0;
+  if (n <= 2 * NJ) return NI + n - 1;
+  return n - 2 * NJ;
+}
+constexpr int RPS = 2;  // LDS reads issued per MFMA slot
+
+// Requantized-output modes (the YQ template argument): no Y; the med3 form
+// for any shift; the int16-saturation form for shifts >= 8, without and with
+// ReLU.
+enum YMode { Y_NONE = 0, Y_MED3 = 1, Y_HI = 2, Y_HI_RELU = 3 };
+
+template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
     int relu) {
   using G = PipeGeom<BM, BN, NW>;
+  constexpr bool WRITE_Y = YQ != Y_NONE;
   __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS_BYTES];
   const uint32_t lds0 = dev::lds_addr(lds);
 
@@ -232,15 +284,24 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
       acc[i][j] = v16i{acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0};
 
   constexpr int CP = G::CP_PER_TILE;
-  // ---- prologue: tiles 0..3 in flight, wait for tile 0
+  // A tile's CP copies go out in two halves, each spread evenly over the
+  // MFMA slots of one phase: the first CP_A in phase 2 of the tile four
+  // earlier (right after the barrier that frees their stage), the other CP_B
+  // in phase 1 of the tile three earlier.  Issuing a whole tile's copies in
+  // one phase saturates the vector-memory path (each copy moves 1 KiB), and
+  // the in-order wave then stalls its MFMAs behind them.
+  constexpr int CP_A = (CP + 1) / 2, CP_B = CP - CP_A;
+
+  // ---- prologue: tiles 0..2 and the first half of tile 3 in flight (tile
+  // 0's phase 1 sends the second half), wait for tile 0
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < KT) {
 #pragma unroll
-      for (int x = 0; x < CP; ++x) copy(s, s, x);
+      for (int x = 0; x < (s == STAGES - 1 ? CP_A : CP); ++x) copy(s, s, x);
     }
   if (KT >= 4)
-    dev::wait_vmcnt<3 * CP>();
+    dev::wait_vmcnt<2 * CP + CP_A>();
   else if (KT == 3)
     dev::wait_vmcnt<2 * CP>();
   else if (KT == 2)
@@ -251,32 +312,54 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
 
   Frags f0, f1;
 #pragma unroll
-  for (int q = 0; q < NREAD; ++q) read_one(0, 0, q, f0);
+  for (int n = 0; n < NREAD; ++n) read_one(0, 0, read_order<G::NI, G::NJ, B_NT>(n), f0);
+
+  // reads of slot x of a phase (RPS per slot, in read_order)
+  auto read_slot = [&](int stage, int ks, int x, Frags& f) {
+#pragma unroll
+    for (int r = 0; r < RPS; ++r)
+      if (RPS * x + r < NREAD) read_one(stage, ks, read_order<G::NI, G::NJ, B_NT>(RPS * x + r), f);
+  };
+  constexpr int READ_SLOTS = (NREAD + RPS - 1) / RPS;
+
+  auto copy_slot = [&](int kt_dst, int stage, int x, int first, int count) {
+#pragma unroll
+    for (int c = 0; c < count; ++c)
+      if ((c * G::NMF) / count == x) copy(kt_dst, stage, first + c);
+  };
 
   // Per tile: phase 1 multiplies k-step 0 (f0) while the reads of k-step 1
-  // (f1) go out between the MFMAs; then the tile barrier; phase 2 multiplies
-  // k-step 1 while the copies of tile kt+4 and the k-step-0 reads of tile
-  // kt+1 go out between the MFMAs.  sched_fence() pins this interleave.
-  // MORE: tile kt+4 exists; NEXT: tile kt+1 exists; VM: copies still allowed
-  // in flight once tile kt+1 has landed.
-  auto tile = [&](int kt, auto more_c, auto next_c, auto vm_c) {
-    constexpr bool MORE = decltype(more_c)::value, NEXT = decltype(next_c)::value;
+  // (f1) and the second half of tile kt+3's copies go out between the MFMAs;
+  // then the tile barrier; phase 2 multiplies k-step 1 while the first half
+  // of tile kt+4's copies and the k-step-0 reads of tile kt+1 go out between
+  // the MFMAs.  sched_fence() pins this interleave.
+  // PRE: tile kt+3 exists (its first half went out in phase 2 of tile kt-1,
+  // or in the prologue for tile 3); MORE: tile kt+4 exists; NEXT: tile kt+1
+  // exists; VM: copies still allowed in flight once tile kt+1 has landed
+  // (those of tiles kt+2 and kt+3, the last ones issued).
+  auto tile = [&](int kt, auto pre_c, auto more_c, auto next_c, auto vm_c) {
+    constexpr bool PRE = decltype(pre_c)::value, MORE = decltype(more_c)::value;
+    constexpr bool NEXT = decltype(next_c)::value;
     constexpr int VM = decltype(vm_c)::value;
     const int cur = kt & (STAGES - 1);
+    // stage of tile kt+3 = stage of tile kt-1, whose last reads completed
+    // before tile kt-1's barrier (for kt = 0: stage 3, not read yet)
+    const int pre_stage = (kt + 3) & (STAGES - 1);
 #pragma unroll
     for (int x = 0; x < G::NMF; ++x) {
       const int i = x / G::NJ, j = x % G::NJ;
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
-      if (x < NREAD) read_one(cur, 1, x, f1);
+      read_slot(cur, 1, x, f1);
+      if constexpr (PRE) copy_slot(kt + 3, pre_stage, x, CP_A, CP_B);
       dev::sched_fence();
     }
-    if constexpr (NREAD > G::NMF) {
+    if constexpr (READ_SLOTS > G::NMF) {
 #pragma unroll
-      for (int q = G::NMF; q < NREAD; ++q) read_one(cur, 1, q, f1);
+      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(cur, 1, x, f1);
     }
     // Tile kt+1 must have landed (own copies, then everyone's via the
     // barrier); after the barrier no wave reads stage `cur` again, so the
-    // copy of tile kt+4 may overwrite it.
+    // copies of tile kt+4 may overwrite it.
     dev::waitcnt<VM, 0>();
     dev::barrier();
     const int nxt = (kt + 1) & (STAGES - 1);
@@ -284,21 +367,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     for (int x = 0; x < G::NMF; ++x) {
       const int i = x / G::NJ, j = x % G::NJ;
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
-      if constexpr (MORE) {
-        if (x < CP) copy(kt + STAGES, cur, x);
-      }
-      if constexpr (NEXT) {
-        if (x < NREAD) read_one(nxt, 0, x, f0);
-      }
+      if constexpr (MORE) copy_slot(kt + STAGES, cur, x, 0, CP_A);
+      if constexpr (NEXT) read_slot(nxt, 0, x, f0);
       dev::sched_fence();
     }
-    if constexpr (MORE && CP > G::NMF) {
+    if constexpr (NEXT && READ_SLOTS > G::NMF) {
 #pragma unroll
-      for (int x = G::NMF; x < CP; ++x) copy(kt + STAGES, cur, x);
-    }
-    if constexpr (NEXT && NREAD > G::NMF) {
-#pragma unroll
-      for (int q = G::NMF; q < NREAD; ++q) read_one(nxt, 0, q, f0);
+      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(nxt, 0, x, f0);
     }
   };
   using T_ = std::true_type;
@@ -307,11 +382,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
   using V1 = std::integral_constant<int, CP>;
   using V0 = std::integral_constant<int, 0>;
   int kt = 0;
-  for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, V2{});
-  if (kt == KT - 4) tile(kt++, F_{}, T_{}, V2{});
-  if (kt == KT - 3) tile(kt++, F_{}, T_{}, V1{});
-  if (kt == KT - 2) tile(kt++, F_{}, T_{}, V0{});
-  tile(kt, F_{}, F_{}, V0{});
+  for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, T_{}, V2{});
+  if (kt == KT - 4) tile(kt++, T_{}, F_{}, T_{}, V2{});
+  if (kt == KT - 3) tile(kt++, F_{}, F_{}, T_{}, V1{});
+  if (kt == KT - 2) tile(kt++, F_{}, F_{}, T_{}, V0{});
+  tile(kt, F_{}, F_{}, F_{}, V0{});
 
   // ---- epilogue.  acc[i][j][4g + t]: row m = wm*WM + 32i + lane%32,
   // column n = wn*WN + 32j + 8g + 4*(lane/32) + t.
@@ -334,21 +409,28 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     // 16-byte stores.  Every LDS read and copy of the main loop completed
     // before its last barrier.
     constexpr int CH = BN / 16;
-    const Requant rq{shift, rnd - acc0, relu ? 0 : -128, 127};
+    auto stage_y = [&](const auto& rq) {
+#pragma unroll
+      for (int i = 0; i < G::NI; ++i)
+#pragma unroll
+        for (int j = 0; j < G::NJ; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int m = wm * G::WM + 32 * i + fr;
+            const int n = wn * G::WN + 32 * j + 8 * g + 4 * fh;
+            const uint32_t packed = rq.pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                             acc[i][j][4 * g + 3]);
+            const int off = m * BN + ((((n >> 4) ^ (m & (CH - 1)))) << 4) + (n & 15);
+            *reinterpret_cast<uint32_t*>(lds + off) = packed;
+          }
+    };
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < G::NI; ++i)
-#pragma unroll
-      for (int j = 0; j < G::NJ; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int m = wm * G::WM + 32 * i + fr;
-          const int n = wn * G::WN + 32 * j + 8 * g + 4 * fh;
-          const uint32_t packed = rq.pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                           acc[i][j][4 * g + 3]);
-          const int off = m * BN + ((((n >> 4) ^ (m & (CH - 1)))) << 4) + (n & 15);
-          *reinterpret_cast<uint32_t*>(lds + off) = packed;
-        }
+    if constexpr (YQ == Y_HI_RELU)
+      stage_y(RequantHi<true>{shift - 8, rnd - acc0});
+    else if constexpr (YQ == Y_HI)
+      stage_y(RequantHi<false>{shift - 8, rnd - acc0});
+    else
+      stage_y(Requant{shift, rnd - acc0, relu ? 0 : -128, 127});
     __syncthreads();
 #pragma unroll
     for (int it = 0; it < BM * CH / G::THREADS; ++it) {
@@ -452,15 +534,24 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
                  int lda, int ldb, int ldy, int ldc, int shift, int relu) {
   constexpr int NW = 4;
   dim3 grid((M / BM) * (N / BN)), block(64 * NW);
-  if (Y && C)
-    hipLaunchKernelGGL((gemm_i8_pipe<BM, BN, NW, B_NT, true, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda,
-                       ldb, ldy, ldc, shift, relu);
-  else if (Y)
-    hipLaunchKernelGGL((gemm_i8_pipe<BM, BN, NW, B_NT, true, false>), grid, block, 0, st, A, B, Y, C, M, N, K, lda,
-                       ldb, ldy, ldc, shift, relu);
-  else
-    hipLaunchKernelGGL((gemm_i8_pipe<BM, BN, NW, B_NT, false, true>), grid, block, 0, st, A, B, Y, C, M, N, K, lda,
-                       ldb, ldy, ldc, shift, relu);
+  const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+  };
+  if (C) {
+    switch (yq) {
+      case Y_NONE: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_NONE, true>); break;
+      case Y_MED3: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_MED3, true>); break;
+      case Y_HI: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI, true>); break;
+      default: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI_RELU, true>); break;
+    }
+  } else {
+    switch (yq) {
+      case Y_MED3: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_MED3, false>); break;
+      case Y_HI: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI, false>); break;
+      default: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI_RELU, false>); break;
+    }
+  }
 }
 
 // Tiling planner for the pipelined kernel: picks the workgroup tile
