@@ -125,14 +125,21 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
     for (int j = 0; j < 4; ++j) acc[i][j] = v16f{0.f};
 
   const int KT = K / BK;
+  // A tile's 8 copies go out in two halves spread over the MFMA slots of one
+  // phase each: the first 4 in phase 2 of the tile four earlier (after the
+  // barrier that frees their stage), the other 4 in phase 1 of the tile three
+  // earlier; a whole tile's copies in one phase saturate the vector-memory
+  // path and stall the in-order wave's MFMAs.  The prologue sends tiles 0..2
+  // and the first half of tile 3; tile 0's phase 1 sends the rest.
+  constexpr int CP_A = CP_PER_TILE / 2, CP_B = CP_PER_TILE - CP_A;
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < KT) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) issue(s, s, i);
+      for (int i = 0; i < (s == STAGES - 1 ? CP_A : CP_PER_TILE); ++i) issue(s, s, i);
     }
   if (KT >= 4)
-    dev::wait_vmcnt<3 * CP_PER_TILE>();
+    dev::wait_vmcnt<2 * CP_PER_TILE + CP_A>();
   else if (KT == 3)
     dev::wait_vmcnt<2 * CP_PER_TILE>();
   else if (KT == 2)
@@ -141,23 +148,43 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
     dev::wait_vmcnt<0>();
   dev::barrier();
 
+  // Reads go out two per MFMA slot in the order the i-major MFMA sequence
+  // first needs them: B0 (two halves), A0, B1 .. B3, A1 .. A3.
+  auto read_n = [](int n) { return n < 2 ? 4 + n : n == 2 ? 0 : n <= 8 ? 3 + n : n - 8; };
   Frags f0, f1;
 #pragma unroll
-  for (int qd = 0; qd < NREAD; ++qd) read_one(0, 0, qd, f0);
+  for (int n = 0; n < NREAD; ++n) read_one(0, 0, read_n(n), f0);
+  auto read_slot = [&](int stage, int ks, int x, Frags& f) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if (2 * x + r < NREAD) read_one(stage, ks, read_n(2 * x + r), f);
+  };
+  auto copy_slot = [&](int kt_dst, int stage, int x, int first) {
+#pragma unroll
+    for (int c = 0; c < CP_A; ++c)
+      if (c * 16 / CP_A == x) issue(kt_dst, stage, first + c);
+  };
 
-  // Phase 1 multiplies k-step 0 while the k-step-1 reads go out; tile
-  // barrier; phase 2 multiplies k-step 1 while the copies of tile kt+4 and
-  // the k-step-0 reads of tile kt+1 go out.
-  auto tile = [&](int kt, auto more_c, auto next_c, auto vm_c) {
-    constexpr bool MORE = decltype(more_c)::value, NEXT = decltype(next_c)::value;
+  // Phase 1 multiplies k-step 0 while the k-step-1 reads and the second half
+  // of tile kt+3's copies go out; tile barrier; phase 2 multiplies k-step 1
+  // while the first half of tile kt+4's copies and the k-step-0 reads of tile
+  // kt+1 go out.  PRE: tile kt+3 exists; MORE: tile kt+4 exists; NEXT: tile
+  // kt+1 exists; VM: copies allowed in flight once tile kt+1 has landed.
+  auto tile = [&](int kt, auto pre_c, auto more_c, auto next_c, auto vm_c) {
+    constexpr bool PRE = decltype(pre_c)::value, MORE = decltype(more_c)::value;
+    constexpr bool NEXT = decltype(next_c)::value;
     constexpr int VM = decltype(vm_c)::value;
     const int cur = kt & (STAGES - 1);
+    // stage of tile kt+3 = stage of tile kt-1, whose reads ended before tile
+    // kt-1's barrier (for kt = 0: stage 3, not read yet)
+    const int pre_stage = (kt + 3) & (STAGES - 1);
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
       const int i = x >> 2, j = x & 3;
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f0, j), __builtin_bit_cast(v8bf, f0.a[i]),
                                                           acc[i][j], 0, 0, 0);
-      if (x < NREAD) read_one(cur, 1, x, f1);
+      read_slot(cur, 1, x, f1);
+      if constexpr (PRE) copy_slot(kt + 3, pre_stage, x, CP_A);
       dev::sched_fence();
     }
     dev::waitcnt<VM, 0>();
@@ -168,12 +195,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
       const int i = x >> 2, j = x & 3;
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f1, j), __builtin_bit_cast(v8bf, f1.a[i]),
                                                           acc[i][j], 0, 0, 0);
-      if constexpr (MORE) {
-        if (x < 8) issue(kt + STAGES, cur, x);
-      }
-      if constexpr (NEXT) {
-        if (x < NREAD) read_one(nxt, 0, x, f0);
-      }
+      if constexpr (MORE) copy_slot(kt + STAGES, cur, x, 0);
+      if constexpr (NEXT) read_slot(nxt, 0, x, f0);
       dev::sched_fence();
     }
   };
@@ -183,11 +206,11 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
   using V1 = std::integral_constant<int, CP_PER_TILE>;
   using V0 = std::integral_constant<int, 0>;
   int kt = 0;
-  for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, V2{});
-  if (kt == KT - 4) tile(kt++, F_{}, T_{}, V2{});
-  if (kt == KT - 3) tile(kt++, F_{}, T_{}, V1{});
-  if (kt == KT - 2) tile(kt++, F_{}, T_{}, V0{});
-  tile(kt, F_{}, F_{}, V0{});
+  for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, T_{}, V2{});
+  if (kt == KT - 4) tile(kt++, T_{}, F_{}, T_{}, V2{});
+  if (kt == KT - 3) tile(kt++, F_{}, F_{}, T_{}, V1{});
+  if (kt == KT - 2) tile(kt++, F_{}, F_{}, T_{}, V0{});
+  tile(kt, F_{}, F_{}, F_{}, V0{});
 
   // acc[i][j][4g + t]: row m = wm*128 + 32i + lane%32, column n = wn*128 + 32j + 8g + 4*(lane/32) + t
 #pragma unroll
