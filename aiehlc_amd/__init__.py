@@ -76,6 +76,7 @@ _SIGS = {
     "miaie_mlp_i8": (_i, [_p, _p, _p, _p, _p, _p] + [_i] * 6),
     "miaie_fill_i8": (_i, [_p, _p, _sz, _u64]),
     "miaie_plan_gemm_i8": (_i, [_p, _i, _i, _i, _p]),
+    "miaie_plan_set_cus": (_i, [_p, _i, C.POINTER(_i)]),
     "miaie_graph_begin": (_i, [_p]),
     "miaie_graph_end": (_i, [_p, C.POINTER(_p)]),
     "miaie_graph_launch": (_i, [_p, _p]),
@@ -281,6 +282,12 @@ class Context:
         plan = GemmPlan()
         self._call("miaie_plan_gemm_i8", M, N, K, C.addressof(plan))
         return plan.as_dict()
+
+    def plan_set_cus(self, cus: int) -> int:
+        """Plan GEMM tiles for `cus` compute units; returns the previous value."""
+        prev = _i(0)
+        self._call("miaie_plan_set_cus", cus, C.byref(prev))
+        return prev.value
 
     def record(self) -> _Recording:
         """`with ctx.record() as g: <entry points>` records them into g

@@ -5,15 +5,19 @@
 // operands and any M, N, K, and of the 64x64 sub-tiling that aiehlc's
 // tiling prototype plans (src/mlir/mlirfront/tilinglinalg/tilinglinalg.cpp:101-103).
 //
-// Two kernels:
-//   gemm_i8_tile256  256x256x64 workgroup tile, 4 waves of 128x128, each a
-//                    4x4 grid of v_mfma_i32_32x32x32_i8.  LDS double buffer
-//                    (the DMA ping-pong of aietypes.td:56-76 / the BD pairs of
-//                    aie_control.cpp:854-875) fed by 128-bit global loads; the
-//                    row-major (NN) B operand is byte-transposed in registers
-//                    with v_perm_b32 on its way to LDS.  XCD-aware tile order.
-//                    Requires M, N % 256 == 0, K % 64 == 0 and aligned strides.
-//   gemm_i8_tile64   64x64x64 tile, bounds-checked, any shape / stride.
+// Kernels:
+//   gemm_i8_pipe    BM x BN x 64 workgroup tiles (256x256, 256x128, 128x128),
+//                   4 waves of BM/2 x BN/2, v_mfma_i32_32x32x32_i8; a 4-stage
+//                   LDS pipeline (the DMA ping-pong of aietypes.td:56-76 / the
+//                   BD pairs of aie_control.cpp:854-875, generalised) filled
+//                   by global_load_lds_dwordx4; the row-major (NN) B operand
+//                   is transposed by ds_read_b64_tr_b8 on its way out of LDS.
+//                   XCD-aware tile order.  M % BM == N % BN == K % 64 == 0.
+//   gemm_i8_pipe2   the same with A staged two k-tiles at a time, so A copies
+//                   move whole cache lines (256-row tiles, K % 128 == 0).
+//   gemm_i8_tile64  64x64x64 tile, bounds-checked, any shape / stride.
+// The requantize epilogue (round, shift, saturate, optional ReLU) is fused
+// into all of them.
 //
 // MFMA operand roles are swapped (srcA = B fragment, srcB = A fragment) so
 // that each lane's accumulator holds 4 consecutive output columns of one row:
@@ -165,6 +169,69 @@ constexpr int RPS = 2;  // LDS reads issued per MFMA slot
 // for any shift; the int16-saturation form for shifts >= 8, without and with
 // ReLU.
 enum YMode { Y_NONE = 0, Y_MED3 = 1, Y_HI = 2, Y_HI_RELU = 3 };
+
+// Epilogue of the pipelined kernels.  acc[i][j][4g + t] holds row
+// m = wm*WM + 32i + lane%32, column n = wn*WN + 32j + 8g + 4*(lane/32) + t of
+// the BM x BN tile.  C (int32) is stored straight from the accumulators; Y is
+// requantized, staged in LDS (16-byte chunk index XOR row%16, within the row's
+// BN/16 chunks) and written with fully coalesced 16-byte stores.  Both stores
+// are non-temporal: nothing in the kernel reads them back, and lines left
+// dirty in L2 are written back when the kernel ends.  `lds` must be free (every
+// LDS read and copy of the main loop completed before its last barrier) and
+// hold BM * BN bytes; rnd_add is the rounding term still to be added.
+template <int BM, int BN, int NW, int YQ, bool WRITE_C, int NI, int NJ>
+__device__ __forceinline__ void pipe_epilogue(v16i (&acc)[NI][NJ], int8_t* lds, int tid, int wm, int wn, int fr,
+                                              int fh, int m0, int n0, int8_t* __restrict__ Y,
+                                              int32_t* __restrict__ C, int ldy, int ldc, int shift, int relu,
+                                              int rnd_add) {
+  constexpr int WM = BM / 2, WN = BN / (NW / 2), THREADS = 64 * NW;
+  if constexpr (WRITE_C) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int m = m0 + wm * WM + 32 * i + fr;
+          const int n = n0 + wn * WN + 32 * j + 8 * g + 4 * fh;
+          v4i v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(C + (size_t)m * ldc + n));
+        }
+  }
+  if constexpr (YQ != Y_NONE) {
+    constexpr int CH = BN / 16;
+    auto stage_y = [&](const auto& rq) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int m = wm * WM + 32 * i + fr;
+            const int n = wn * WN + 32 * j + 8 * g + 4 * fh;
+            const uint32_t packed = rq.pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                             acc[i][j][4 * g + 3]);
+            const int off = m * BN + ((((n >> 4) ^ (m & (CH - 1)))) << 4) + (n & 15);
+            *reinterpret_cast<uint32_t*>(lds + off) = packed;
+          }
+    };
+    __syncthreads();
+    if constexpr (YQ == Y_HI_RELU)
+      stage_y(RequantHi<true>{shift - 8, rnd_add});
+    else if constexpr (YQ == Y_HI)
+      stage_y(RequantHi<false>{shift - 8, rnd_add});
+    else
+      stage_y(Requant{shift, rnd_add, relu ? 0 : -128, 127});
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < BM * CH / THREADS; ++it) {
+      const int flat = it * THREADS + tid;
+      const int m = flat / CH, c = flat % CH;
+      const v4i v = *reinterpret_cast<const v4i*>(lds + m * BN + ((c ^ (m & (CH - 1))) << 4));
+      __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + c * 16));
+    }
+  }
+}
 
 template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
@@ -388,58 +455,310 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
   if (kt == KT - 2) tile(kt++, F_{}, F_{}, T_{}, V0{});
   tile(kt, F_{}, F_{}, F_{}, V0{});
 
-  // ---- epilogue.  acc[i][j][4g + t]: row m = wm*WM + 32i + lane%32,
-  // column n = wn*WN + 32j + 8g + 4*(lane/32) + t.
-  if constexpr (WRITE_C) {
-#pragma unroll
-    for (int i = 0; i < G::NI; ++i)
-#pragma unroll
-      for (int j = 0; j < G::NJ; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int m = m0 + wm * G::WM + 32 * i + fr;
-          const int n = n0 + wn * G::WN + 32 * j + 8 * g + 4 * fh;
-          v4i v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          *reinterpret_cast<v4i*>(C + (size_t)m * ldc + n) = v;
-        }
+  pipe_epilogue<BM, BN, NW, YQ, WRITE_C>(acc, lds, tid, wm, wn, fr, fh, m0, n0, Y, C, ldy, ldc, shift, relu,
+                                        rnd - acc0);
+}
+
+// ------------------------------------------------------ pair-staged tile
+// gemm_i8_pipe with A staged two k-tiles at a time.  A row-major A tile
+// row contributes 64 bytes per k-tile, so a per-k-tile copy touches every
+// 128-byte line at half use; the L1 fetches whole lines, the address path
+// handles 16 lines per 1 KiB copy, and the A stream costs twice its bytes on
+// the L2 -> L1 path.  Here A lives in NA2 = 3 pair stages of BM rows x 128
+// bytes (k-tiles 2p and 2p+1 of pair p in stage p % 3) and each 1 KiB copy
+// moves 8 whole lines; B keeps its four per-k-tile stages.  Needs K % 128 == 0.
+//
+// Copy schedule, in phases phi = 2t + (h - 1) (tile t, phase h = 1, 2):
+//   B tile k: first half at phi = 2k - 7 (phase 2 of tile k-4, after the
+//     barrier that retires tile k-4's reads of its stage), second half at
+//     phi = 2k - 6 (phase 1 of tile k-3);
+//   A pair p: quarter q at phi = 4p - 9 + q (phase 2 of tile 2p-5, after the
+//     barrier that retires pair p-3's reads of its stage, through phase 1 of
+//     tile 2p-3).
+// Copies with phi < 0 go out in the prologue, in phi order.  Tile t's data
+// (B tile t, A pair t/2) was issued by phase 2t - 6, so the barrier of tile
+// t-1 (end of phase 2t - 2) waits until at most the copies of the four phases
+// after it are in flight: 2 * (copies per tile) in steady state, fewer in the
+// last tiles (pipe2_vm).
+constexpr int NA2 = 3;
+
+template <int BM, int BN, int NW>
+struct Pipe2Geom {
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int WAVES_N = NW / 2;
+  static constexpr int WM = BM / 2, WN = BN / WAVES_N;
+  static constexpr int NI = WM / 32, NJ = WN / 32, NMF = NI * NJ;
+  static constexpr int A2_BYTES = BM * 128;                 // one A pair stage
+  static constexpr int A_REGION = NA2 * A2_BYTES;
+  static constexpr int B_BYTES = BN * BK;                   // one B stage
+  static constexpr int LDS_BYTES = A_REGION + STAGES * B_BYTES;
+  static constexpr int CP_BYTES = 1024 * NW;                // one 16-byte copy by every thread
+  static constexpr int A_CP2 = A2_BYTES / CP_BYTES;         // A copies per thread per pair
+  static constexpr int QA = A_CP2 / 4;                      // ... per quarter (per phase)
+  static constexpr int B_CP = B_BYTES / CP_BYTES;           // B copies per thread per k-tile
+  static constexpr int B_CP0 = (B_CP + 1) / 2, B_CP1 = B_CP - B_CP0;
+  static constexpr int CP = A_CP2 / 2 + B_CP;               // copies per thread per k-tile
+  static_assert(NI >= 1 && NJ >= 1 && B_CP >= 1 && A_CP2 % 4 == 0 && QA >= 1, "pair-staged geometry");
+  static_assert(LDS_BYTES <= 163840 && BM * BN <= LDS_BYTES, "pair-staged LDS budget");
+};
+
+// Copies issued in phase h of the tile d tiles before the last (KT even, so
+// that tile is even exactly when d is odd); tiles with d >= 6 issue all.
+template <int BM, int BN, int NW>
+constexpr int pipe2_phase_copies(int d, int h) {
+  using G = Pipe2Geom<BM, BN, NW>;
+  if (h == 1) return (d >= 3 ? G::B_CP1 : 0) + (((d & 1) ? d >= 5 : d >= 4) ? G::QA : 0);
+  return (d >= 4 ? G::B_CP0 : 0) + (((d & 1) ? d >= 5 : d >= 6) ? G::QA : 0);
+}
+// Copies allowed in flight at the barrier of the tile d before the last: those
+// of the four phases after the phase that issued the next tile's last copy.
+template <int BM, int BN, int NW>
+constexpr int pipe2_vm(int d) {
+  return pipe2_phase_copies<BM, BN, NW>(d + 2, 2) + pipe2_phase_copies<BM, BN, NW>(d + 1, 1) +
+         pipe2_phase_copies<BM, BN, NW>(d + 1, 2) + pipe2_phase_copies<BM, BN, NW>(d, 1);
+}
+
+template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
+    int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
+    int relu) {
+  using G = Pipe2Geom<BM, BN, NW>;
+  constexpr bool WRITE_Y = YQ != Y_NONE;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS_BYTES];
+  const uint32_t lds0 = dev::lds_addr(lds);
+  int8_t* const bl = lds + G::A_REGION;  // B stages
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  int tm, tn;
+  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KT = K / BK;  // even
+
+  // ---- copy assignment.  A copy x of wave w fills the 1 KiB block NW*x + w
+  // of a pair stage: rows 8*(NW*x + w) + lane/8, physical chunk lane%8 of the
+  // row's 128 bytes, holding logical chunk (lane%8) ^ aswz(row) with
+  // aswz(row) = (row >> 1) & 7 (= 4*(w&1) + lane/16 for every x).  The MFMA
+  // fragment read (16 consecutive rows at one logical chunk) then touches 16
+  // distinct 16-byte bank groups.  B copies as in gemm_i8_pipe.
+  const int a_r = 8 * wave + (lane >> 3);
+  const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 7) ^ ((a_r >> 1) & 7));
+  const int8_t* const a_base = A + (size_t)m0 * lda;
+  uint32_t b_voff;
+  const int8_t* b_base;
+  constexpr int B_ROWS_PER_CP = B_NT ? 16 * NW : 1024 * NW / BN;
+  if constexpr (B_NT) {
+    const int b_r = 16 * wave + (lane >> 2);
+    b_voff = (uint32_t)b_r * ldb + 16 * ((lane & 3) ^ swz(b_r));
+    b_base = B + (size_t)n0 * ldb;
+  } else {
+    constexpr int CPR = BN / 16;
+    const int b_r = (1024 / BN) * wave + lane / CPR;
+    b_voff = (uint32_t)b_r * ldb + 16 * ((lane % CPR) ^ bswz<BN>(b_r));
+    b_base = B + n0;
   }
-  if constexpr (WRITE_Y) {
-    // Stage the 256 x BN int8 tile in LDS (16-byte chunk index XOR row%16,
-    // within the row's BN/16 chunks), then write it out with fully coalesced
-    // 16-byte stores.  Every LDS read and copy of the main loop completed
-    // before its last barrier.
-    constexpr int CH = BN / 16;
-    auto stage_y = [&](const auto& rq) {
+  // copy x (< A_CP2) of A pair p; copy x (< B_CP) of B k-tile kt
+  auto copy_a = [&](int p, int x) {
+    const uint32_t st = lds0 + (p % NA2) * G::A2_BYTES + 1024 * wave + G::CP_BYTES * x;
+    dev::gload_lds16(a_base + (size_t)p * 128 + (size_t)(8 * NW * x) * lda, a_voff, st);
+  };
+  auto copy_b = [&](int kt, int x) {
+    const uint32_t st = lds0 + G::A_REGION + (kt & (STAGES - 1)) * G::B_BYTES + 1024 * wave + G::CP_BYTES * x;
+    const int8_t* bb = B_NT ? b_base + (size_t)kt * BK : b_base + (size_t)kt * BK * ldb;
+    dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * x) * ldb, b_voff, st);
+  };
+
+  // ---- fragment offsets.  A fragment (par, ks, i) of k-tile 2p + par: row
+  // wm*WM + 32i + lane%32 of pair stage p % 3, logical chunk 4par + 2ks +
+  // lane/32, physical chunk XOR (row >> 1) & 7 = (lane%32 >> 1) & 7.
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+  const int fr = lane & 31, fh = lane >> 5;
+  int a_fo[2][2], b_fo[G::NJ > 2 ? G::NJ : 2];
 #pragma unroll
-      for (int i = 0; i < G::NI; ++i)
+  for (int par = 0; par < 2; ++par)
 #pragma unroll
-        for (int j = 0; j < G::NJ; ++j)
+    for (int ks = 0; ks < 2; ++ks)
+      a_fo[par][ks] = (wm * G::WM + fr) * 128 + (((4 * par + 2 * ks + fh) ^ ((fr >> 1) & 7)) << 4);
+  if constexpr (B_NT) {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int m = wm * G::WM + 32 * i + fr;
-            const int n = wn * G::WN + 32 * j + 8 * g + 4 * fh;
-            const uint32_t packed = rq.pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                             acc[i][j][4 * g + 3]);
-            const int off = m * BN + ((((n >> 4) ^ (m & (CH - 1)))) << 4) + (n & 15);
-            *reinterpret_cast<uint32_t*>(lds + off) = packed;
-          }
-    };
-    __syncthreads();
-    if constexpr (YQ == Y_HI_RELU)
-      stage_y(RequantHi<true>{shift - 8, rnd - acc0});
-    else if constexpr (YQ == Y_HI)
-      stage_y(RequantHi<false>{shift - 8, rnd - acc0});
-    else
-      stage_y(Requant{shift, rnd - acc0, relu ? 0 : -128, 127});
-    __syncthreads();
+    for (int ks = 0; ks < 2; ++ks) b_fo[ks] = (wn * G::WN + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+  } else {
+    // tr8 halves as in gemm_i8_pipe
+    const int g = lane >> 4, jj = (lane >> 1) & 7, h = lane & 1;
 #pragma unroll
-    for (int it = 0; it < BM * CH / G::THREADS; ++it) {
-      const int flat = it * G::THREADS + tid;
-      const int m = flat / CH, c = flat % CH;
-      const v4i v = *reinterpret_cast<const v4i*>(lds + m * BN + ((c ^ (m & (CH - 1))) << 4));
-      *reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + c * 16) = v;
+    for (int j = 0; j < G::NJ; ++j) {
+      const int c = wn * (G::WN / 16) + 2 * j + (g & 1);
+      b_fo[j] = (16 * (g >> 1) + jj) * BN + ((c ^ bswz<BN>(jj)) << 4) + 8 * h;
     }
   }
+
+  struct Frags {
+    v4i a[G::NI];
+    v4i b[G::NJ];
+    miaie_v2i lo[G::NJ], hi[G::NJ];
+  };
+  constexpr int NREAD = G::NI + (B_NT ? 1 : 2) * G::NJ;
+  // q-th LDS read of k-step ks of k-tile kt (parity PAR) into f
+  auto read_one = [&](int kt, auto par_c, int ks, int q, Frags& f) {
+    constexpr int PAR = decltype(par_c)::value;
+    if (q < G::NI) {
+      const int8_t* s = lds + ((kt >> 1) % NA2) * G::A2_BYTES;
+      f.a[q] = *reinterpret_cast<const v4i*>(s + a_fo[PAR][ks] + 4096 * q);
+    } else {
+      const int8_t* s = bl + (kt & (STAGES - 1)) * G::B_BYTES;
+      if constexpr (B_NT) {
+        f.b[q - G::NI] = *reinterpret_cast<const v4i*>(s + b_fo[ks] + 2048 * (q - G::NI));
+      } else {
+        const int j = (q - G::NI) >> 1;
+        if (((q - G::NI) & 1) == 0)
+          f.lo[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN);
+        else
+          f.hi[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN + 8 * BN);
+      }
+    }
+  };
+  auto bfrag = [&](const Frags& f, int j) -> v4i {
+    if constexpr (B_NT)
+      return f.b[j];
+    else
+      return v4i{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
+  };
+  constexpr int READ_SLOTS = (NREAD + RPS - 1) / RPS;
+  auto read_slot = [&](int kt, auto par_c, int ks, int x, Frags& f) {
+#pragma unroll
+    for (int r = 0; r < RPS; ++r)
+      if (RPS * x + r < NREAD) read_one(kt, par_c, ks, read_order<G::NI, G::NJ, B_NT>(RPS * x + r), f);
+  };
+
+  const int rnd = shift ? 1 << (shift - 1) : 0;
+  const int acc0 = (WRITE_Y && !WRITE_C) ? rnd : 0;
+  v16i acc[G::NI][G::NJ];
+#pragma unroll
+  for (int i = 0; i < G::NI; ++i)
+#pragma unroll
+    for (int j = 0; j < G::NJ; ++j)
+      acc[i][j] = v16i{acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0};
+
+  // ---- prologue: phases -9 .. -1 in order (B tiles 0..2, the first half of
+  // B tile 3, A pairs 0 and 1, the first quarter of A pair 2), then wait for
+  // B tile 0 and A pair 0 (issued by phase -6).
+  const int KP = KT / 2;
+#pragma unroll
+  for (int phi = -9; phi < 0; ++phi) {
+    if ((phi & 1) != 0) {
+      const int k = (phi + 7) / 2;  // B first half
+      if (phi >= -7 && k < KT)
+#pragma unroll
+        for (int x = 0; x < G::B_CP0; ++x) copy_b(k, x);
+    } else {
+      const int k = (phi + 6) / 2;  // B second half
+      if (phi >= -6 && k < KT)
+#pragma unroll
+        for (int x = G::B_CP0; x < G::B_CP; ++x) copy_b(k, x);
+    }
+    const int p = (phi + 9) / 4, q = (phi + 9) % 4;
+    if (p < KP)
+#pragma unroll
+      for (int x = 0; x < G::QA; ++x) copy_a(p, G::QA * q + x);
+  }
+  if (KT >= 6)
+    dev::wait_vmcnt<2 * G::B_CP + G::B_CP0 + 5 * G::QA>();
+  else
+    dev::wait_vmcnt<0>();
+  dev::barrier();
+
+  Frags f0, f1;
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+#pragma unroll
+  for (int n = 0; n < NREAD; ++n) read_one(0, P0{}, 0, read_order<G::NI, G::NJ, B_NT>(n), f0);
+
+  // The copies of one phase: nb B copies (first_b ..) of k-tile kb and na A
+  // copies (first_a ..) of pair pa, spread evenly over the MFMA slots.
+  auto copy_slot = [&](int x, int kb, int first_b, int nb, int pa, int first_a, int na) {
+#pragma unroll
+    for (int c = 0; c < nb + na; ++c)
+      if ((c * G::NMF) / (nb + na) == x) {
+        if (c < nb)
+          copy_b(kb, first_b + c);
+        else
+          copy_a(pa, first_a + c - nb);
+      }
+  };
+
+  // Tile t (parity PAR, D tiles before the last; D >= 6 for every tile of the
+  // steady loop): phase 1 multiplies k-step 0 while the k-step-1 reads and
+  // the phase's copies go out; barrier; phase 2 multiplies k-step 1 while the
+  // phase's copies and tile t+1's k-step-0 reads go out.
+  auto tile = [&](int t, auto par_c, auto d_c) {
+    constexpr int PAR = decltype(par_c)::value, D = decltype(d_c)::value;
+    constexpr int NB1 = D >= 3 ? G::B_CP1 : 0, NB2 = D >= 4 ? G::B_CP0 : 0;
+    constexpr int NA1 = (PAR == 0 ? D >= 5 : D >= 4) ? G::QA : 0;
+    constexpr int NA2_ = (PAR == 0 ? D >= 5 : D >= 6) ? G::QA : 0;
+    constexpr bool NEXT = D >= 1;
+    constexpr int VM = pipe2_vm<BM, BN, NW>(D);
+    // phase 1: B k-tile t+3 (second half); A pair t/2+2 quarter 1 (t even) or
+    // pair (t+3)/2 quarter 3 (t odd)
+    const int pa1 = PAR == 0 ? (t >> 1) + 2 : (t + 3) >> 1;
+    constexpr int qa1 = PAR == 0 ? 1 : 3;
+#pragma unroll
+    for (int x = 0; x < G::NMF; ++x) {
+      const int i = x / G::NJ, j = x % G::NJ;
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
+      read_slot(t, par_c, 1, x, f1);
+      copy_slot(x, t + 3, G::B_CP0, NB1, pa1, G::QA * qa1, NA1);
+      dev::sched_fence();
+    }
+    if constexpr (READ_SLOTS > G::NMF) {
+#pragma unroll
+      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(t, par_c, 1, x, f1);
+    }
+    // next k-tile's data has landed (own copies, then everyone's via the
+    // barrier); after the barrier no wave reads this tile's B stage again
+    dev::waitcnt<VM, 0>();
+    dev::barrier();
+    // phase 2: B k-tile t+4 (first half); A pair t/2+2 quarter 2 (t even) or
+    // pair (t+5)/2 quarter 0 (t odd)
+    const int pa2 = PAR == 0 ? (t >> 1) + 2 : (t + 5) >> 1;
+    constexpr int qa2 = PAR == 0 ? 2 : 0;
+    using PN = std::integral_constant<int, 1 - PAR>;
+#pragma unroll
+    for (int x = 0; x < G::NMF; ++x) {
+      const int i = x / G::NJ, j = x % G::NJ;
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
+      copy_slot(x, t + 4, 0, NB2, pa2, G::QA * qa2, NA2_);
+      if constexpr (NEXT) read_slot(t + 1, PN{}, 0, x, f0);
+      dev::sched_fence();
+    }
+    if constexpr (NEXT && READ_SLOTS > G::NMF) {
+#pragma unroll
+      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(t + 1, PN{}, 0, x, f0);
+    }
+  };
+  using DS = std::integral_constant<int, 64>;  // steady state
+  int t = 0;
+  for (; t + 6 < KT; t += 2) {
+    tile(t, P0{}, DS{});
+    tile(t + 1, P1{}, DS{});
+  }
+  if (KT >= 6) {
+    tile(t, P0{}, std::integral_constant<int, 5>{});
+    tile(t + 1, P1{}, std::integral_constant<int, 4>{});
+    t += 2;
+  }
+  if (KT >= 4) {
+    tile(t, P0{}, std::integral_constant<int, 3>{});
+    tile(t + 1, P1{}, std::integral_constant<int, 2>{});
+    t += 2;
+  }
+  tile(t, P0{}, std::integral_constant<int, 1>{});
+  tile(t + 1, P1{}, std::integral_constant<int, 0>{});
+
+  pipe_epilogue<BM, BN, NW, YQ, WRITE_C>(acc, lds, tid, wm, wn, fr, fh, m0, n0, Y, C, ldy, ldc, shift, relu,
+                                        rnd - acc0);
 }
 
 // ------------------------------------------------------------ 64x64 tile
@@ -538,6 +857,29 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
   };
+  // 256-row tiles with K a multiple of 128: A staged two k-tiles at a time
+  // (gemm_i8_pipe2; 256x256 4096^3 68.9 -> 66.4 us, the MLP's 256x128
+  // projections 6-10% faster).  At 128x128, where half the CUs run at a higher
+  // clock, it measured 4% slower, so that tile keeps gemm_i8_pipe.
+  if constexpr (BM == 256) {
+    if (K % 128 == 0) {
+      if (C) {
+        switch (yq) {
+          case Y_NONE: go(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_NONE, true>); break;
+          case Y_MED3: go(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_MED3, true>); break;
+          case Y_HI: go(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_HI, true>); break;
+          default: go(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_HI_RELU, true>); break;
+        }
+      } else {
+        switch (yq) {
+          case Y_MED3: go(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_MED3, false>); break;
+          case Y_HI: go(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_HI, false>); break;
+          default: go(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_HI_RELU, false>); break;
+        }
+      }
+      return;
+    }
+  }
   if (C) {
     switch (yq) {
       case Y_NONE: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_NONE, true>); break;

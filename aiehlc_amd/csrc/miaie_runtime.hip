@@ -314,6 +314,15 @@ extern "C" int miaie_plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, miaie_gem
   return plan_gemm_i8(ctx, M, N, K, (K % 16 == 0) && (N % 16 == 0) && K < (1 << 16), plan);
 }
 
+extern "C" int miaie_plan_set_cus(miaie_ctx* ctx, int cus, int* previous) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (cus < 1) return fail(ctx, MIAIE_EINVAL, "miaie_plan_set_cus: cus=%d", cus);
+  if (previous) *previous = ctx->cus;
+  ctx->cus = cus;
+  return MIAIE_OK;
+}
+
 // ---------------------------------------------------------------- recorded chains
 struct miaie_graph {
   int device = 0;

@@ -109,6 +109,13 @@ typedef struct {
 } miaie_gemm_plan;
 MIAIE_API int miaie_plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, miaie_gemm_plan* plan);
 
+/* The number of compute units the planner distributes tiles over on this
+ * context (the reference prototype's thread count, numThreads = {8, 16} at
+ * src/mlir/mlirfront/tilinglinalg/tilinglinalg.cpp:101).  It starts at the
+ * device's CU count; a caller sharing the GPU with other streams can plan for
+ * fewer.  cus >= 1; *previous (nullable) receives the old value. */
+MIAIE_API int miaie_plan_set_cus(miaie_ctx* ctx, int cus, int* previous);
+
 /* ---- recorded kernel chains --------------------------------------------- */
 
 /* The reference chains kernels through the host: run k1, wait, move k1's

@@ -28,6 +28,16 @@ def test_planner_choices(ctx):
     assert ctx.plan_gemm_i8(100, 50, 30)["kernel"] == mi.KERNEL_TILE64
     assert ctx.plan_gemm_i8(128, 128, 100)["kernel"] == mi.KERNEL_TILE64
     assert ctx.call_status("miaie_plan_gemm_i8", 0, 1, 1, None) == mi.MIAIE_EINVAL
+    # planning for fewer CUs: one CU takes the widest tile that fits
+    prev = ctx.plan_set_cus(1)
+    try:
+        assert (ctx.plan_gemm_i8(512, 512, 256)["tile_m"], ctx.plan_gemm_i8(512, 512, 256)["tile_n"]) == (256, 256)
+        assert ctx.plan_gemm_i8(256, 384, 256)["tile_n"] == 128
+        assert ctx.plan_gemm_i8(128, 256, 256)["tile_m"] == 128
+    finally:
+        assert ctx.plan_set_cus(prev) == 1
+    assert ctx.plan_gemm_i8(4096, 4096, 4096)["tile_n"] == 256
+    assert ctx.call_status("miaie_plan_set_cus", 0, None) == mi.MIAIE_EINVAL
 
 
 SHAPES = [(512, 4096, 4096, mi.B_NN), (256, 1024, 2048, mi.B_NT), (128, 2048, 1024, mi.B_NN),
@@ -64,3 +74,54 @@ def test_128_tiles_match_the_oracle(ctx, M, N, K, layout):
         ctx.gemm_i8_i32(dAh, dB, dCh, M, N, K, b_layout=layout)
         ctx.wait(60_000)
         assert np.array_equal(ctx.download(dC), 2 * ctx.download(dCh))
+
+
+# K sweep over the pipelined kernels: K % 128 == 0 takes the pair-staged
+# kernel (A staged two k-tiles at a time, a copy schedule whose waits change
+# over the last six k-tiles and in the prologue below 6 k-tiles), other
+# multiples of 64 the per-k-tile kernel.  Every k-tile count from the
+# smallest up to well past the steady state, at each tile width (planned for
+# one CU, M x N picks 256x256, 256x128 and 128x128), both B layouts and every
+# output mode.
+K_SWEEP = [64, 128, 192, 256, 320, 384, 512, 640, 768, 896, 1024, 1152, 1280, 2176, 2240]
+TILE_SHAPES = [(512, 512), (256, 384), (128, 256)]
+
+
+@pytest.mark.parametrize("K", K_SWEEP)
+@pytest.mark.parametrize("MN", TILE_SHAPES)
+@pytest.mark.parametrize("layout", [mi.B_NN, mi.B_NT])
+def test_pipelined_k_sweep(ctx, K, MN, layout):
+    M, N = MN
+    # planning for one CU makes the planner take the widest tile that fits
+    prev = ctx.plan_set_cus(1)
+    try:
+        _k_sweep(ctx, M, N, K, MN, layout)
+    finally:
+        ctx.plan_set_cus(prev)
+
+
+def _k_sweep(ctx, M, N, K, MN, layout):
+    plan = ctx.plan_gemm_i8(M, N, K)
+    print(f"[case] k-sweep gemm {M}x{N}x{K} layout {layout} plan {plan}", flush=True)
+    assert plan["kernel"] == mi.KERNEL_PIPE
+    assert (plan["tile_m"], plan["tile_n"]) == {(512, 512): (256, 256), (256, 384): (256, 128),
+                                                (128, 256): (128, 128)}[MN]
+    rng = np.random.default_rng(7 * K + M + layout)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(N, K) if layout == mi.B_NT else (K, N), dtype=np.int8)
+    dA, dB = ctx.upload(A), ctx.upload(B)
+    dC, dY, dY2, dC2, dY3 = (ctx.empty((M, N), np.int32), ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int8),
+                             ctx.empty((M, N), np.int32), ctx.empty((M, N), np.int8))
+    ctx.gemm_i8_i32(dA, dB, dC, M, N, K, b_layout=layout)          # C only
+    ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, layout)    # Y only, shift >= 8
+    ctx.gemm_i8_rq(dA, dB, dY2, M, N, K, 11, True, dC2, layout)     # Y + C, ReLU
+    ctx.gemm_i8_rq(dA, dB, dY3, M, N, K, 5, True, None, layout)     # Y only, shift < 8, ReLU
+    ctx.wait(60_000)
+    C = ctx.download(dC)
+    assert np.array_equal(C, oracle.gemm_i8(A, B, b_nt=layout == mi.B_NT))
+    assert np.array_equal(ctx.download(dY), oracle.requant(C, 10))
+    assert np.array_equal(ctx.download(dY2), oracle.requant(C, 11, relu=True))
+    assert np.array_equal(ctx.download(dC2), C)
+    assert np.array_equal(ctx.download(dY3), oracle.requant(C, 5, relu=True))
+    for b in (dA, dB, dC, dY, dY2, dC2, dY3):
+        b.free()
