@@ -226,6 +226,222 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
       }
 }
 
+// Pair-staged variant (K % 64 == 0): A in three LDS stages of 256 rows x 128
+// bytes (two k-tiles, 64 bf16 of k), so each A copy moves whole 128-byte lines
+// instead of touching 16 lines at half use; B keeps four per-k-tile stages
+// (32 k-rows of 512 bytes, whole lines already).  160 KiB of LDS.  The copy
+// schedule is the int8 pair-staged kernel's (dev::pair_vm): B k-tile k in two
+// halves at phases 2k-7 and 2k-6, A pair p in quarters at phases 4p-9+q.
+// A pair-stage row r holds logical 16-byte chunk c at c ^ ((r >> 1) & 7), so
+// a fragment read (16 consecutive rows, one logical chunk) touches 16
+// distinct bank groups.
+constexpr int NA2 = 3;
+constexpr int A2_BYTES = BM * 128;                  // one A pair stage (32 KiB)
+constexpr int A_REGION = NA2 * A2_BYTES;            // 96 KiB
+constexpr int B_BYTES = BK * BN * 2;                // one B stage (16 KiB)
+constexpr int PAIR_LDS = A_REGION + STAGES * B_BYTES;
+constexpr int A_CP2 = A2_BYTES / 4096, QA = A_CP2 / 4;  // A copies per thread per pair / per phase
+constexpr int B_CP = B_BYTES / 4096, B_CP0 = (B_CP + 1) / 2, B_CP1 = B_CP - B_CP0;
+static_assert(PAIR_LDS <= 163840, "pair-staged LDS budget");
+
+__global__ __launch_bounds__(256, 1) void gemm_bf16_pair(const uint16_t* __restrict__ A,
+                                                         const uint16_t* __restrict__ B,
+                                                         float* __restrict__ C, int M, int N, int K) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[PAIR_LDS];
+  const uint32_t lds0 = dev::lds_addr(lds);
+  int8_t* const bl = lds + A_REGION;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  int tm, tn;
+  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const size_t lda = (size_t)K * 2, ldb = (size_t)N * 2;  // row pitches in bytes
+  const int KT = K / BK;                                   // even
+
+  // A copy x of wave w: rows 8(4x + w) + lane/8, physical chunk lane%8 of the
+  // row's 128 bytes (logical chunk (lane%8) ^ ((row >> 1) & 7), the same for
+  // every x).  B copy i: k-rows 8i + 2w + lane/32, physical chunk lane%32.
+  const int a_r = 8 * wave + (lane >> 3);
+  const uint32_t a_voff = (uint32_t)(a_r * lda) + 16 * ((lane & 7) ^ ((a_r >> 1) & 7));
+  const int8_t* const a_base = reinterpret_cast<const int8_t*>(A) + (size_t)m0 * lda;
+  const int b_r = 2 * wave + (lane >> 5);
+  const uint32_t b_voff = (uint32_t)(b_r * ldb) + 16 * ((lane & 31) ^ ((b_r & 3) << 2));
+  const int8_t* const b_base = reinterpret_cast<const int8_t*>(B) + (size_t)n0 * 2;
+  auto copy_a = [&](int p, int x) {
+    dev::gload_lds16(a_base + (size_t)p * 128 + (size_t)(32 * x) * lda, a_voff,
+                     lds0 + (p % NA2) * A2_BYTES + 1024 * wave + 4096 * x);
+  };
+  auto copy_b = [&](int kt, int i) {
+    dev::gload_lds16(b_base + (size_t)kt * BK * ldb + (size_t)(8 * i) * ldb, b_voff,
+                     lds0 + A_REGION + (kt & (STAGES - 1)) * B_BYTES + 1024 * wave + 4096 * i);
+  };
+
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fr = lane & 31, fh = lane >> 5;
+  int a_fo[2][2], b_fo[4];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      a_fo[par][ks] = (wm * 128 + fr) * 128 + (((4 * par + 2 * ks + fh) ^ ((fr >> 1) & 7)) << 4);
+  {
+    // tr16 halves as in gemm_bf16_tile256, relative to the B stage
+    const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = wn * 16 + 4 * j + 2 * (g & 1) + (q >> 1);
+      b_fo[j] = (8 * (g >> 1) + jj) * 512 + ((c ^ (jj << 2)) << 4) + 8 * (q & 1);
+    }
+  }
+  struct Frags {
+    v4i a[4];
+    miaie_v4s lo[4], hi[4];
+  };
+  constexpr int NREAD = 12;
+  auto read_one = [&](int kt, auto par_c, int ks, int qd, Frags& f) {
+    constexpr int PAR = decltype(par_c)::value;
+    if (qd < 4) {
+      f.a[qd] = *reinterpret_cast<const v4i*>(lds + ((kt >> 1) % NA2) * A2_BYTES + a_fo[PAR][ks] + 4096 * qd);
+    } else {
+      const int8_t* s = bl + (kt & (STAGES - 1)) * B_BYTES;
+      const int j = (qd - 4) >> 1;
+      if ((qd & 1) == 0)
+        f.lo[j] = dev::lds_read_tr16(s + b_fo[j] + ks * 8192);
+      else
+        f.hi[j] = dev::lds_read_tr16(s + b_fo[j] + ks * 8192 + 2048);
+    }
+  };
+  auto bfrag = [&](const Frags& f, int j) -> v8bf {
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s v = {f.lo[j][0], f.lo[j][1], f.lo[j][2], f.lo[j][3], f.hi[j][0], f.hi[j][1], f.hi[j][2], f.hi[j][3]};
+    return __builtin_bit_cast(v8bf, v);
+  };
+  // reads two per MFMA slot in first-use order: B0 (two halves), A0, B1 .. B3, A1 .. A3
+  auto read_n = [](int n) { return n < 2 ? 4 + n : n == 2 ? 0 : n <= 8 ? 3 + n : n - 8; };
+  auto read_slot = [&](int kt, auto par_c, int ks, int x, Frags& f) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if (2 * x + r < NREAD) read_one(kt, par_c, ks, read_n(2 * x + r), f);
+  };
+
+  v16f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v16f{0.f};
+
+  // prologue: phases -9 .. -1 in order, then wait for B k-tile 0 and A pair 0
+  const int KP = KT / 2;
+#pragma unroll
+  for (int phi = -9; phi < 0; ++phi) {
+    if ((phi & 1) != 0) {
+      const int kb = (phi + 7) / 2;
+      if (phi >= -7 && kb < KT)
+#pragma unroll
+        for (int x = 0; x < B_CP0; ++x) copy_b(kb, x);
+    } else {
+      const int kb = (phi + 6) / 2;
+      if (phi >= -6 && kb < KT)
+#pragma unroll
+        for (int x = B_CP0; x < B_CP; ++x) copy_b(kb, x);
+    }
+    const int p = (phi + 9) / 4, q = (phi + 9) % 4;
+    if (p < KP)
+#pragma unroll
+      for (int x = 0; x < QA; ++x) copy_a(p, QA * q + x);
+  }
+  if (KT >= 6)
+    dev::wait_vmcnt<dev::pair_prologue_vm(B_CP0, B_CP1, QA)>();
+  else
+    dev::wait_vmcnt<0>();
+  dev::barrier();
+
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  Frags f0, f1;
+#pragma unroll
+  for (int n = 0; n < NREAD; ++n) read_one(0, P0{}, 0, read_n(n), f0);
+
+  auto copy_slot = [&](int x, int kb, int first_b, int nb, int pa, int first_a, int na) {
+#pragma unroll
+    for (int c = 0; c < nb + na; ++c)
+      if ((c * 16) / (nb + na) == x) {
+        if (c < nb)
+          copy_b(kb, first_b + c);
+        else
+          copy_a(pa, first_a + c - nb);
+      }
+  };
+  // k-tile t (parity PAR, D k-tiles before the last; D >= 6 in the steady loop)
+  auto tile = [&](int t, auto par_c, auto d_c) {
+    constexpr int PAR = decltype(par_c)::value, D = decltype(d_c)::value;
+    constexpr int NB1 = D >= 3 ? B_CP1 : 0, NB2 = D >= 4 ? B_CP0 : 0;
+    constexpr int NA1 = (PAR == 0 ? D >= 5 : D >= 4) ? QA : 0;
+    constexpr int NA2_ = (PAR == 0 ? D >= 5 : D >= 6) ? QA : 0;
+    constexpr bool NEXT = D >= 1;
+    constexpr int VM = dev::pair_vm(D, B_CP0, B_CP1, QA);
+    const int pa1 = PAR == 0 ? (t >> 1) + 2 : (t + 3) >> 1;
+    constexpr int qa1 = PAR == 0 ? 1 : 3;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int i = x >> 2, j = x & 3;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f0, j), __builtin_bit_cast(v8bf, f0.a[i]),
+                                                          acc[i][j], 0, 0, 0);
+      read_slot(t, par_c, 1, x, f1);
+      copy_slot(x, t + 3, B_CP0, NB1, pa1, QA * qa1, NA1);
+      dev::sched_fence();
+    }
+    dev::waitcnt<VM, 0>();
+    dev::barrier();
+    const int pa2 = PAR == 0 ? (t >> 1) + 2 : (t + 5) >> 1;
+    constexpr int qa2 = PAR == 0 ? 2 : 0;
+    using PN = std::integral_constant<int, 1 - PAR>;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int i = x >> 2, j = x & 3;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f1, j), __builtin_bit_cast(v8bf, f1.a[i]),
+                                                          acc[i][j], 0, 0, 0);
+      copy_slot(x, t + 4, 0, NB2, pa2, QA * qa2, NA2_);
+      if constexpr (NEXT) read_slot(t + 1, PN{}, 0, x, f0);
+      dev::sched_fence();
+    }
+  };
+  using DS = std::integral_constant<int, 64>;  // steady state
+  int t = 0;
+  for (; t + 6 < KT; t += 2) {
+    tile(t, P0{}, DS{});
+    tile(t + 1, P1{}, DS{});
+  }
+  if (KT >= 6) {
+    tile(t, P0{}, std::integral_constant<int, 5>{});
+    tile(t + 1, P1{}, std::integral_constant<int, 4>{});
+    t += 2;
+  }
+  if (KT >= 4) {
+    tile(t, P0{}, std::integral_constant<int, 3>{});
+    tile(t + 1, P1{}, std::integral_constant<int, 2>{});
+    t += 2;
+  }
+  tile(t, P0{}, std::integral_constant<int, 1>{});
+  tile(t + 1, P1{}, std::integral_constant<int, 0>{});
+
+  // acc[i][j][4g + t]: row m = wm*128 + 32i + lane%32, column n = wn*128 + 32j + 8g + 4*(lane/32) + t;
+  // non-temporal stores (nothing in the kernel reads C back)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int m = m0 + wm * 128 + 32 * i + fr;
+        const int n = n0 + wn * 128 + 32 * j + 8 * g + 4 * fh;
+        v4f v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(C + (size_t)m * N + n));
+      }
+}
+
 __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restrict__ A,
                                                         const uint16_t* __restrict__ B,
                                                         float* __restrict__ C, int M, int N, int K) {
@@ -287,6 +503,10 @@ int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float
   // offsets of up to 64 rows in 32 bits.
   const bool big = M % BM == 0 && N % BN == 0 && K % BK == 0 && aligned(A, 16) && aligned(B, 16) &&
                    aligned(C, 16) && K < (1 << 24) && N < (1 << 24);
+  if (big && K % (2 * BK) == 0) {
+    hipLaunchKernelGGL(gemm_bf16_pair, dim3((M / BM) * (N / BN)), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
+    return check_launch(ctx, "gemm_bf16_pair");
+  }
   if (big) {
     hipLaunchKernelGGL(gemm_bf16_tile256, dim3((M / BM) * (N / BN)), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
     return check_launch(ctx, "gemm_bf16_tile256");

@@ -479,7 +479,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
 // (B tile t, A pair t/2) was issued by phase 2t - 6, so the barrier of tile
 // t-1 (end of phase 2t - 2) waits until at most the copies of the four phases
 // after it are in flight: 2 * (copies per tile) in steady state, fewer in the
-// last tiles (pipe2_vm).
+// last tiles (dev::pair_vm).
 constexpr int NA2 = 3;
 
 template <int BM, int BN, int NW>
@@ -501,22 +501,6 @@ struct Pipe2Geom {
   static_assert(NI >= 1 && NJ >= 1 && B_CP >= 1 && A_CP2 % 4 == 0 && QA >= 1, "pair-staged geometry");
   static_assert(LDS_BYTES <= 163840 && BM * BN <= LDS_BYTES, "pair-staged LDS budget");
 };
-
-// Copies issued in phase h of the tile d tiles before the last (KT even, so
-// that tile is even exactly when d is odd); tiles with d >= 6 issue all.
-template <int BM, int BN, int NW>
-constexpr int pipe2_phase_copies(int d, int h) {
-  using G = Pipe2Geom<BM, BN, NW>;
-  if (h == 1) return (d >= 3 ? G::B_CP1 : 0) + (((d & 1) ? d >= 5 : d >= 4) ? G::QA : 0);
-  return (d >= 4 ? G::B_CP0 : 0) + (((d & 1) ? d >= 5 : d >= 6) ? G::QA : 0);
-}
-// Copies allowed in flight at the barrier of the tile d before the last: those
-// of the four phases after the phase that issued the next tile's last copy.
-template <int BM, int BN, int NW>
-constexpr int pipe2_vm(int d) {
-  return pipe2_phase_copies<BM, BN, NW>(d + 2, 2) + pipe2_phase_copies<BM, BN, NW>(d + 1, 1) +
-         pipe2_phase_copies<BM, BN, NW>(d + 1, 2) + pipe2_phase_copies<BM, BN, NW>(d, 1);
-}
 
 template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
@@ -665,7 +649,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
       for (int x = 0; x < G::QA; ++x) copy_a(p, G::QA * q + x);
   }
   if (KT >= 6)
-    dev::wait_vmcnt<2 * G::B_CP + G::B_CP0 + 5 * G::QA>();
+    dev::wait_vmcnt<dev::pair_prologue_vm(G::B_CP0, G::B_CP1, G::QA)>();
   else
     dev::wait_vmcnt<0>();
   dev::barrier();
@@ -699,7 +683,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
     constexpr int NA1 = (PAR == 0 ? D >= 5 : D >= 4) ? G::QA : 0;
     constexpr int NA2_ = (PAR == 0 ? D >= 5 : D >= 6) ? G::QA : 0;
     constexpr bool NEXT = D >= 1;
-    constexpr int VM = pipe2_vm<BM, BN, NW>(D);
+    constexpr int VM = dev::pair_vm(D, G::B_CP0, G::B_CP1, G::QA);
     // phase 1: B k-tile t+3 (second half); A pair t/2+2 quarter 1 (t even) or
     // pair (t+3)/2 quarter 3 (t odd)
     const int pa1 = PAR == 0 ? (t >> 1) + 2 : (t + 3) >> 1;

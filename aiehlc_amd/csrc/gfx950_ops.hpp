@@ -71,6 +71,30 @@ __device__ __forceinline__ miaie_v4s lds_read_tr16(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((MIAIE_LDS miaie_v4s*)(p));
 }
 
+// Copy schedule of the pair-staged pipelines: A in three LDS stages of two
+// k-tiles each, B in four per-k-tile stages.  In phases phi = 2t + h - 1
+// (k-tile t, phase h = 1, 2), B k-tile k goes out in two halves, b_cp0
+// copies at phi = 2k - 7 and b_cp1 at phi = 2k - 6; A pair p (k-tiles 2p,
+// 2p+1) in quarters of qa copies at phi = 4p - 9 + q; phases before 0 belong
+// to the prologue.  pair_phase_copies: copies issued in phase h of the
+// k-tile d before the last (the k-tile count is even, so that k-tile is even
+// exactly when d is odd); every k-tile with d >= 6 issues all of them.
+constexpr int pair_phase_copies(int d, int h, int b_cp0, int b_cp1, int qa) {
+  if (h == 1) return (d >= 3 ? b_cp1 : 0) + (((d & 1) ? d >= 5 : d >= 4) ? qa : 0);
+  return (d >= 4 ? b_cp0 : 0) + (((d & 1) ? d >= 5 : d >= 6) ? qa : 0);
+}
+// Copies allowed in flight at the barrier of the k-tile d before the last:
+// those of the four phases after the one that issued the next k-tile's last
+// copy (B k-tile t+1 at phase 2t - 4, A pair (t+1)/2 no later).
+constexpr int pair_vm(int d, int b_cp0, int b_cp1, int qa) {
+  return pair_phase_copies(d + 2, 2, b_cp0, b_cp1, qa) + pair_phase_copies(d + 1, 1, b_cp0, b_cp1, qa) +
+         pair_phase_copies(d + 1, 2, b_cp0, b_cp1, qa) + pair_phase_copies(d, 1, b_cp0, b_cp1, qa);
+}
+// Copies allowed in flight after the prologue (phases -5 .. -1), once B
+// k-tile 0 and A pair 0 (issued by phase -6) have landed; valid for 6 or more
+// k-tiles.
+constexpr int pair_prologue_vm(int b_cp0, int b_cp1, int qa) { return 2 * (b_cp0 + b_cp1) + b_cp0 + 5 * qa; }
+
 // Tile order.  Workgroups are dealt round-robin to the 8 XCDs, so workgroup
 // b runs on XCD b % 8.  Give each XCD a contiguous run of logical tiles, and
 // walk logical tiles in groups of GROUP_M tile-rows, column by column, so one

@@ -148,6 +148,28 @@ def test_gemm_bf16(ctx, shape):
     assert err <= 1e-5, err
 
 
+# K sweep over the 256x256 bf16 kernels: K % 64 == 0 takes the pair-staged
+# kernel (A staged two k-tiles at a time; its waits change over the last six
+# k-tiles and in the prologue below six), odd multiples of 32 the per-k-tile
+# kernel.
+@pytest.mark.parametrize("K", [32, 64, 96, 128, 192, 256, 320, 384, 448, 512, 576, 1088, 2112])
+def test_gemm_bf16_k_sweep(ctx, K):
+    M, N = 512, 256
+    _say("gemm_bf16 k-sweep", (M, N, K))
+    A = synth.bf16_normal((M, K), 5, 1.0 / np.sqrt(K))
+    B = synth.bf16_normal((K, N), 6, 1.0 / np.sqrt(K))
+    dA, dB, dC = ctx.upload(A), ctx.upload(B), ctx.empty((M, N), np.float32)
+    ctx.gemm_bf16_f32(dA, dB, dC, M, N, K)
+    ctx.wait(60_000)
+    Cg = ctx.download(dC).astype(np.float64)
+    for b in (dA, dB, dC):
+        b.free()
+    R = oracle.gemm_bf16(A, B, f64=True)
+    err = np.abs(Cg - R).max() / np.abs(R).max()
+    assert err <= BF16_TOL, err
+    assert err <= 1e-5, err
+
+
 def test_gemm_bf16_8192_config(ctx):
     """Config 3: 8192^3 bf16, N(0,1)/sqrt(K).  Normwise error on a 32-row slab
     and 32 scattered rows against the fp64 oracle."""
