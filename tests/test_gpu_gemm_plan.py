@@ -125,3 +125,37 @@ def _k_sweep(ctx, M, N, K, MN, layout):
     assert np.array_equal(ctx.download(dY3), oracle.requant(C, 5, relu=True))
     for b in (dA, dB, dC, dY, dY2, dC2, dY3):
         b.free()
+
+
+# Operands inside larger row-major arrays (row pitch > the product's extent):
+# 16-byte multiples keep the pipelined kernels (per-k-tile and pair-staged),
+# other pitches take the bounds-checked 64x64 kernel.  C = A.B is checked on
+# the product's rows and columns, and C's padding must stay untouched.
+@pytest.mark.parametrize("M,N,K,lda,ldb,ldc,layout", [
+    (512, 512, 256, 320, 640, 528, mi.B_NN),   # pair-staged 256x256
+    (512, 512, 256, 336, 272, 520, mi.B_NT),
+    (512, 512, 192, 208, 528, 512, mi.B_NN),   # per-k-tile 256x256 (K % 128 != 0)
+    (256, 384, 384, 400, 400, 392, mi.B_NN),   # 256x128
+    (128, 256, 256, 288, 304, 260, mi.B_NT),   # 128x128
+    (128, 256, 256, 260, 256, 256, mi.B_NN),   # lda % 16 != 0: fallback
+])
+def test_strided_operands(ctx, M, N, K, lda, ldb, ldc, layout):
+    prev = ctx.plan_set_cus(1)
+    try:
+        print(f"[case] strided gemm {M}x{N}x{K} lda {lda} ldb {ldb} ldc {ldc} layout {layout}", flush=True)
+        rng = np.random.default_rng(lda + ldb + ldc + layout)
+        Ab = rng.integers(-128, 128, size=(M, lda), dtype=np.int8)
+        Bb = rng.integers(-128, 128, size=(N, ldb) if layout == mi.B_NT else (K, ldb), dtype=np.int8)
+        Cb = np.full((M, ldc), 0x5A5A5A5A, dtype=np.int32)
+        dA, dB, dC = ctx.upload(Ab), ctx.upload(Bb), ctx.upload(Cb)
+        ctx.gemm_i8_i32(dA, dB, dC, M, N, K, lda=lda, ldb=ldb, ldc=ldc, b_layout=layout)
+        ctx.wait(60_000)
+        Cg = ctx.download(dC)
+        A = np.ascontiguousarray(Ab[:, :K])
+        B = np.ascontiguousarray(Bb[:, :K] if layout == mi.B_NT else Bb[:, :N])
+        assert np.array_equal(Cg[:, :N], oracle.gemm_i8(A, B, b_nt=layout == mi.B_NT))
+        assert (Cg[:, N:] == 0x5A5A5A5A).all()
+        for b in (dA, dB, dC):
+            b.free()
+    finally:
+        ctx.plan_set_cus(prev)
