@@ -200,6 +200,10 @@ CONV_SHAPES = [
     (1, 7, 64, 64, 128, 3, 3, 1, 1),  # odd Ho, Wo = 64, two Cout blocks
     (3, 5, 33, 32, 64, 3, 3, 1, 0),   # no padding
     (2, 56, 56, 64, 64, 3, 3, 1, 1),  # config shape, fewer images
+    (1, 5, 48, 64, 64, 3, 3, 1, 1),   # row-pair kernel: odd Ho (last workgroup half outside the image)
+    (2, 6, 50, 64, 128, 3, 3, 1, 0),  # row-pair, no padding, two Cout blocks
+    (1, 9, 60, 64, 64, 3, 3, 1, 2),   # row-pair, pad 2 (two zero columns each side)
+    (1, 4, 64, 64, 64, 3, 3, 1, 0),   # row-pair, widest row, no padding
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # fallback kernel (channels not multiples of 32/64)
     (2, 6, 7, 3, 5, 3, 3, 2, 0),      # fallback kernel
 ]
