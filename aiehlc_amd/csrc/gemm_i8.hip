@@ -610,11 +610,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
     else
       return v4i{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
   };
-  constexpr int READ_SLOTS = (NREAD + RPS - 1) / RPS;
+  // LDS reads per MFMA slot: one at 256x256 (16 slots for 12 reads; 1152
+  // against 1190 cycles per k-tile with two), two at 256x128 (8 slots for 8
+  // reads; 655 against 669 with one)
+  constexpr int RPS2 = G::NMF >= 16 ? 1 : 2;
+  constexpr int READ_SLOTS = (NREAD + RPS2 - 1) / RPS2;
   auto read_slot = [&](int kt, auto par_c, int ks, int x, Frags& f) {
 #pragma unroll
-    for (int r = 0; r < RPS; ++r)
-      if (RPS * x + r < NREAD) read_one(kt, par_c, ks, read_order<G::NI, G::NJ, B_NT>(RPS * x + r), f);
+    for (int r = 0; r < RPS2; ++r)
+      if (RPS2 * x + r < NREAD) read_one(kt, par_c, ks, read_order<G::NI, G::NJ, B_NT>(RPS2 * x + r), f);
   };
 
   const int rnd = shift ? 1 << (shift - 1) : 0;
