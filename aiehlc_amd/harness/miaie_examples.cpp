@@ -195,6 +195,9 @@ int run_gemm(miaie::Context& ctx, int M, int N, int K, int shift) {
     }
   printf("int8 GEMM %dx%dx%d shift %d: %.1f us incl. launch and wait (%.1f TOP/s)\n", M, N, K, shift, us,
          2.0 * M * N * K / us / 1e6);
+  const miaie_gemm_plan plan = ctx.plan_gemm_i8(M, N, K);
+  printf("plan: kernel %d, tile %dx%d, %d workgroups of %d threads\n", plan.kernel, plan.tile_m, plan.tile_n,
+         plan.workgroups, plan.threads);
   return report(mismatches, "gemm");
 }
 

@@ -85,6 +85,18 @@ class Context {
     check(rc);
     return true;
   }
+  // The tiling planner: the kernel, tile and grid an int8 GEMM of this shape
+  // takes, and the CU count it plans for (returns the previous one).
+  miaie_gemm_plan plan_gemm_i8(int M, int N, int K) const {
+    miaie_gemm_plan p{};
+    check(miaie_plan_gemm_i8(h_, M, N, K, &p));
+    return p;
+  }
+  int plan_set_cus(int cus) const {
+    int prev = 0;
+    check(miaie_plan_set_cus(h_, cus, &prev));
+    return prev;
+  }
 
  private:
   miaie_ctx* h_ = nullptr;

@@ -40,3 +40,5 @@ def test_harness_example(args, needle):
     print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
     assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
     assert needle in r.stdout
+    if args[:4] == ["gemm", "4096", "4096", "4096"]:  # the planner, read through miaie::Context
+        assert "plan: kernel 1, tile 256x256, 256 workgroups of 256 threads" in r.stdout
