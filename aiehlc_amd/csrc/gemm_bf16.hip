@@ -7,8 +7,10 @@
 // Same geometry as the int8 kernel: a row of an LDS tile is 64 bytes
 // (32 bf16 of k), read as 16-byte MFMA fragments with the same XOR swizzle;
 // the row-major B operand is 16-bit-transposed in registers on its way to LDS.
-//   gemm_bf16_tile256  256x256x32, 4 waves x (4x4 MFMA 32x32x16), LDS double buffer.
+//   gemm_bf16_pair     256x256, K % 64 == 0: A staged two k-tiles at a time.
+//   gemm_bf16_tile256  256x256x32, 4 waves x (4x4 MFMA 32x32x16), four LDS stages.
 //   gemm_bf16_tile64   64x64x32 bounds-checked fallback.
+// Both 256x256 kernels write C through store_tile_f32 (whole-row stores).
 #include <type_traits>
 
 #include "gfx950_ops.hpp"
@@ -25,6 +27,46 @@ __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + ((chunk ^ swz(row)) << 4); }
 
 __device__ __forceinline__ v8bf as_bf(v4i x) { return __builtin_bit_cast(v8bf, x); }
+
+// fp32 epilogue of a 256x256 tile held as acc[i][j][4g + t] = C[m0 + wm*128
+// + 32i + lane%32][n0 + wn*128 + 32j + 8g + 4*(lane/32) + t], staged through
+// 128 KiB of LDS in two halves so that every store instruction writes one
+// whole 1 KiB row (eight full 128-byte lines).  Direct stores from the
+// accumulators write 32 bytes per row per instruction; with every workgroup
+// of a round storing at once, that burst cost 5% of the 8192^3 GEMM, this one
+// half of that.  Half h holds each wave's row blocks i = 2h, 2h+1: LDS row
+// R = wm*64 + 32(i - 2h) + lane%32 (tile row wm*128 + 64h + R%64), logical
+// 16-byte chunk c at physical chunk c ^ (R & 15), so both the column writes
+// (16 rows, one chunk) and the row reads (one row, 16 chunks) touch 16
+// distinct bank groups.  Stores are non-temporal: nothing reads C back.
+__device__ __forceinline__ void store_tile_f32(const v16f (&acc)[4][4], int8_t* lds, int wave, int lane, float* C,
+                                               int m0, int n0, int N) {
+  const int wm = wave >> 1, wn = wave & 1, fr = lane & 31, fh = lane >> 5;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    dev::barrier();  // the other waves' last reads of this LDS (k-loop fragments or the previous half)
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const v16f& a = acc[2 * h + ii][j];
+          const int R = wm * 64 + 32 * ii + fr;
+          const int c = wn * 32 + 8 * j + 2 * g + fh;
+          const v4f v = {a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+          *reinterpret_cast<v4f*>(lds + R * 1024 + ((c ^ (R & 15)) << 4)) = v;
+        }
+    dev::barrier();
+#pragma unroll
+    for (int rr = 0; rr < 32; ++rr) {
+      const int R = wave * 32 + rr;
+      const v4f v = *reinterpret_cast<const v4f*>(lds + R * 1024 + ((lane ^ (R & 15)) << 4));
+      const int m = m0 + (R >> 6) * 128 + 64 * h + (R & 63);
+      __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(C + (size_t)m * N + n0 + 4 * lane));
+    }
+  }
+}
 
 // 256x256 workgroup tile, k-step 32, four 32 KiB LDS stages fed by
 // global_load_lds_dwordx4 (the AIE ping-pong generalised to depth 4), one
@@ -212,18 +254,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
   if (kt == KT - 2) tile(kt++, F_{}, F_{}, T_{}, V0{});
   tile(kt, F_{}, F_{}, F_{}, V0{});
 
-  // acc[i][j][4g + t]: row m = wm*128 + 32i + lane%32, column n = wn*128 + 32j + 8g + 4*(lane/32) + t
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int m = m0 + wm * 128 + 32 * i + fr;
-        const int n = n0 + wn * 128 + 32 * j + 8 * g + 4 * fh;
-        v4f v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-        *reinterpret_cast<v4f*>(C + (size_t)m * N + n) = v;
-      }
+  store_tile_f32(acc, lds, wave, lane, C, m0, n0, N);
 }
 
 // Pair-staged variant (K % 64 == 0): A in three LDS stages of 256 rows x 128
@@ -427,19 +458,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair(const uint16_t* __restr
   tile(t, P0{}, std::integral_constant<int, 1>{});
   tile(t + 1, P1{}, std::integral_constant<int, 0>{});
 
-  // acc[i][j][4g + t]: row m = wm*128 + 32i + lane%32, column n = wn*128 + 32j + 8g + 4*(lane/32) + t;
-  // non-temporal stores (nothing in the kernel reads C back)
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int m = m0 + wm * 128 + 32 * i + fr;
-        const int n = n0 + wn * 128 + 32 * j + 8 * g + 4 * fh;
-        v4f v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-        __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(C + (size_t)m * N + n));
-      }
+  store_tile_f32(acc, lds, wave, lane, C, m0, n0, N);
 }
 
 __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restrict__ A,
