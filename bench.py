@@ -15,6 +15,10 @@ Also in the line (not the headline):
                          sharded over M, with the tile the planner picks
   extras.mfma_ceiling    register-only MFMA rate on this GPU, constant and
                          random operands (aiehlc_amd/probes/mfma_ceiling)
+  extras.launch_floor    time per back-to-back launch of an empty kernel with the
+                         conv's and the GEMM's grid and LDS size
+                         (aiehlc_amd/probes/launch_floor); the conv line carries
+                         its own floor and the time above it
   extras.vendor_library  the same int8 4096^3 and bf16 8192^3 products through
                          hipBLASLt (torch._int_mm / torch.matmul) on this GPU
   cpu_baseline           the reference's CPU golden loop (i-j-k, int32
@@ -47,6 +51,7 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_rq_4096_traffic.txt")
 CEILING_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "mfma_ceiling")
+FLOOR_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "launch_floor")
 METRIC = "int8 GEMM TOPS (% MFMA peak) at 4096^3; int8 conv2d 3x3 GOPS; vs host CPU"
 
 
@@ -217,13 +222,18 @@ def other_cpu_goldens(threads: int) -> dict:
     return out
 
 
-def mfma_ceiling() -> dict | None:
-    if not os.path.exists(CEILING_EXE):
+def probe_json(exe: str) -> dict | None:
+    """Run one of the standalone probes (aiehlc_amd/probes) and parse its JSON."""
+    if not os.path.exists(exe):
         return None
-    r = subprocess.run([CEILING_EXE], capture_output=True, text=True, timeout=120)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     if r.returncode != 0:
         return {"error": r.stderr.strip()[-300:]}
     return json.loads(r.stdout)
+
+
+def mfma_ceiling() -> dict | None:
+    return probe_json(CEILING_EXE)
 
 
 def vendor_library(steps: int) -> dict:
@@ -405,6 +415,14 @@ def main() -> int:
     ctx.close()
     if not args.no_extras:
         extras["mfma_ceiling"] = mfma_ceiling()
+        floor = probe_json(FLOOR_EXE)
+        extras["launch_floor"] = floor
+        conv = extras.get("conv2d_3x3")
+        cf = (floor or {}).get("conv2d_rows_grid")
+        if conv and isinstance(cf, dict):
+            # the same grid and LDS with an empty kernel body, in its own process
+            conv["launch_floor_us"] = cf["us_per_launch"]
+            conv["us_above_floor"] = round(conv["us_per_step"] - cf["us_per_launch"], 3)
         extras["vendor_library"] = vendor_library(args.steps)
 
     roofline = {
