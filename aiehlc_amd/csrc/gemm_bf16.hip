@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
     dev::wait_vmcnt<0>();
   dev::barrier();
 
-  // Reads go out two per MFMA slot in the order the i-major MFMA sequence
+  // Reads go out two per MFMA slot in the order the MFMA sequence
   // first needs them: B0 (two halves), A0, B1 .. B3, A1 .. A3.
   auto read_n = [](int n) { return n < 2 ? 4 + n : n == 2 ? 0 : n <= 8 ? 3 + n : n - 8; };
   Frags f0, f1;
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
     const int pre_stage = (kt + 3) & (STAGES - 1);
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
-      const int i = x >> 2, j = x & 3;
+      const int i = x >> 2, j = dev::snake_j<4>(x);
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f0, j), __builtin_bit_cast(v8bf, f0.a[i]),
                                                           acc[i][j], 0, 0, 0);
       read_slot(cur, 1, x, f1);
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
     const int nxt = (kt + 1) & (STAGES - 1);
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
-      const int i = x >> 2, j = x & 3;
+      const int i = x >> 2, j = dev::snake_j<4>(x);
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f1, j), __builtin_bit_cast(v8bf, f1.a[i]),
                                                           acc[i][j], 0, 0, 0);
       if constexpr (MORE) copy_slot(kt + STAGES, cur, x, 0);
@@ -417,7 +417,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair(const uint16_t* __restr
     constexpr int qa1 = PAR == 0 ? 1 : 3;
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
-      const int i = x >> 2, j = x & 3;
+      const int i = x >> 2, j = dev::snake_j<4>(x);
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f0, j), __builtin_bit_cast(v8bf, f0.a[i]),
                                                           acc[i][j], 0, 0, 0);
       read_slot(t, par_c, 1, x, f1);
@@ -431,7 +431,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair(const uint16_t* __restr
     using PN = std::integral_constant<int, 1 - PAR>;
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
-      const int i = x >> 2, j = x & 3;
+      const int i = x >> 2, j = dev::snake_j<4>(x);
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f1, j), __builtin_bit_cast(v8bf, f1.a[i]),
                                                           acc[i][j], 0, 0, 0);
       copy_slot(x, t + 4, 0, NB2, pa2, QA * qa2, NA2_);

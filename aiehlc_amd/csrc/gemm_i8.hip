@@ -145,8 +145,8 @@ __device__ __forceinline__ int bswz(int k) {
 // Issue order of one k-step's LDS reads.  Reads are numbered as in
 // read_one (A fragment i -> i; NT B fragment j -> NI + j; NN B fragment j ->
 // NI + 2j and NI + 2j + 1, its two transposing halves), and go out in the
-// order the i-major MFMA sequence (i, j) = (x / NJ, x % NJ) first needs them:
-// B0, A0, B1 .. B(NJ-1), A1 .. A(NI-1).  With reads issued RPS per MFMA slot
+// order the MFMA sequence (i, j) = (x / NJ, dev::snake_j<NJ>(x)) first needs
+// them: B0, A0, B1 .. B(NJ-1), A1 .. A(NI-1).  With reads issued RPS per MFMA slot
 // from the start of a phase, every fragment has landed several MFMAs before
 // the next phase consumes it, and the last read of a phase is far from the
 // wait that precedes the tile barrier.
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     const int pre_stage = (kt + 3) & (STAGES - 1);
 #pragma unroll
     for (int x = 0; x < G::NMF; ++x) {
-      const int i = x / G::NJ, j = x % G::NJ;
+      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
       read_slot(cur, 1, x, f1);
       if constexpr (PRE) copy_slot(kt + 3, pre_stage, x, CP_A, CP_B);
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     const int nxt = (kt + 1) & (STAGES - 1);
 #pragma unroll
     for (int x = 0; x < G::NMF; ++x) {
-      const int i = x / G::NJ, j = x % G::NJ;
+      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
       if constexpr (MORE) copy_slot(kt + STAGES, cur, x, 0, CP_A);
       if constexpr (NEXT) read_slot(nxt, 0, x, f0);
@@ -694,7 +694,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
     constexpr int qa1 = PAR == 0 ? 1 : 3;
 #pragma unroll
     for (int x = 0; x < G::NMF; ++x) {
-      const int i = x / G::NJ, j = x % G::NJ;
+      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
       read_slot(t, par_c, 1, x, f1);
       copy_slot(x, t + 3, G::B_CP0, NB1, pa1, G::QA * qa1, NA1);
@@ -715,7 +715,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
     using PN = std::integral_constant<int, 1 - PAR>;
 #pragma unroll
     for (int x = 0; x < G::NMF; ++x) {
-      const int i = x / G::NJ, j = x % G::NJ;
+      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
       copy_slot(x, t + 4, 0, NB2, pa2, G::QA * qa2, NA2_);
       if constexpr (NEXT) read_slot(t + 1, PN{}, 0, x, f0);

@@ -95,6 +95,18 @@ constexpr int pair_vm(int d, int b_cp0, int b_cp1, int qa) {
 // k-tiles.
 constexpr int pair_prologue_vm(int b_cp0, int b_cp1, int qa) { return 2 * (b_cp0 + b_cp1) + b_cp0 + 5 * qa; }
 
+// MFMA order within a wave tile of NI x NJ blocks: slot x runs block
+// (x / NJ, snake_j(x)), rows in order and columns serpentine (reversed on odd
+// rows), so every MFMA shares one operand with the one before it (A within a
+// row, B at a row turn).  Fewer operand bits toggle, and under the power
+// limit the clock runs higher: register-only streams of random int8 operands
+// ran 0.6% faster in this order than in plain row-major order, and 2.2%
+// faster than with both operands changing every MFMA.
+template <int NJ>
+constexpr int snake_j(int x) {
+  return ((x / NJ) & 1) ? NJ - 1 - x % NJ : x % NJ;
+}
+
 // Tile order.  Workgroups are dealt round-robin to the 8 XCDs, so workgroup
 // b runs on XCD b % 8.  Give each XCD a contiguous run of logical tiles, and
 // walk logical tiles in groups of GROUP_M tile-rows, column by column, so one
