@@ -359,7 +359,11 @@ extern "C" int miaie_graph_end(miaie_ctx* ctx, miaie_graph** out) {
     return fail(ctx, MIAIE_EINVAL, "miaie_graph_end: graph is NULL (the recording is discarded)");
   }
   *out = nullptr;
-  miaie_graph* mg = new miaie_graph;
+  miaie_graph* mg = new (std::nothrow) miaie_graph;
+  if (!mg) {
+    (void)hipGraphDestroy(g);
+    return fail(ctx, MIAIE_ENOMEM, "miaie_graph_end: host allocation failed");
+  }
   mg->device = ctx->device;
   mg->graph = g;
   (void)hipGraphGetNodes(g, nullptr, &mg->nodes);

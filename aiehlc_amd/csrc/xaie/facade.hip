@@ -127,6 +127,17 @@ u32 builtin_extent(const XAie_MiaieKernel* k, u32 param, u32 arg) {
 }
 
 thread_local std::string g_last_error;
+
+// Every entry point runs inside a function-try-block: a host allocation that
+// fails in the bookkeeping (std::bad_alloc) becomes XAIE_ERR (or NULL), not an
+// exception crossing the C ABI.
+AieRC out_of_memory(const char* fn) noexcept {
+  try {
+    g_last_error = std::string(fn) + ": out of host memory";
+  } catch (...) {
+  }
+  return XAIE_ERR;
+}
 std::vector<miaie_xaie_dev*> g_devices;  // initialised instances, for XAie_MiaieRunOnDdr
 
 enum TileKind { T_NONE, T_SHIM, T_MEM, T_CORE };
@@ -459,25 +470,25 @@ void reset_state(miaie_xaie_dev* d) {
 // ======================================================================== C ABI
 extern "C" {
 
-MIAIE_XAIE_API AieRC XAie_MiaieWindowLayout(const XAie_MiaieKernel* Kernel, u32* Ping, u32* Pong) {
+MIAIE_XAIE_API AieRC XAie_MiaieWindowLayout(const XAie_MiaieKernel* Kernel, u32* Ping, u32* Pong) try {
   const XAie_MiaieKernel* k = nullptr;
   if (AieRC rc = valid_kernel(nullptr, Kernel, &k)) return rc;
   window_layout(k, Ping, Pong);
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API const char* XAie_MiaieLastError(const XAie_DevInst* DevInst) {
+MIAIE_XAIE_API const char* XAie_MiaieLastError(const XAie_DevInst* DevInst) try {
   if (DevInst && DevInst->IsReady && DevInst->Priv) return DevInst->Priv->err.c_str();
   return g_last_error.c_str();
-}
+} catch (...) { out_of_memory(__func__); return nullptr; }
 
-MIAIE_XAIE_API u32 XAie_MiaieTileMemBytes(const XAie_DevInst* DevInst, XAie_LocType Loc) {
+MIAIE_XAIE_API u32 XAie_MiaieTileMemBytes(const XAie_DevInst* DevInst, XAie_LocType Loc) try {
   if (!DevInst || !DevInst->IsReady || !DevInst->Priv) return 0;
   const int t = tile_index(DevInst->Priv, Loc);
   return t < 0 ? 0 : DevInst->Priv->bytes[t];
-}
+} catch (...) { out_of_memory(__func__); return 0; }
 
-MIAIE_XAIE_API AieRC XAie_SetupPartitionConfig(XAie_DevInst* DevInst, u64 PartBaseAddr, u32 StartCol, u32 NumCols) {
+MIAIE_XAIE_API AieRC XAie_SetupPartitionConfig(XAie_DevInst* DevInst, u64 PartBaseAddr, u32 StartCol, u32 NumCols) try {
   if (!DevInst) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_SetupPartitionConfig: DevInst is NULL");
   if (DevInst->IsReady) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_SetupPartitionConfig: already initialised");
   if (NumCols == 0 || NumCols > 255 || StartCol > 255)
@@ -486,9 +497,9 @@ MIAIE_XAIE_API AieRC XAie_SetupPartitionConfig(XAie_DevInst* DevInst, u64 PartBa
   DevInst->PartNumCols = (u8)NumCols;
   DevInst->PartBaseAddr = PartBaseAddr;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_CfgInitialize(XAie_DevInst* DevInst, const XAie_Config* Cfg) {
+MIAIE_XAIE_API AieRC XAie_CfgInitialize(XAie_DevInst* DevInst, const XAie_Config* Cfg) try {
   if (!DevInst || !Cfg) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_CfgInitialize: NULL argument");
   if (DevInst->IsReady) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_CfgInitialize: instance already initialised");
   if (Cfg->NumCols == 0 || Cfg->NumRows == 0 || Cfg->ShimRowNum >= Cfg->NumRows ||
@@ -575,9 +586,9 @@ MIAIE_XAIE_API AieRC XAie_CfgInitialize(XAie_DevInst* DevInst, const XAie_Config
   DevInst->IsReady = 1;
   g_devices.push_back(d);
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_SetIOBackend(XAie_DevInst* DevInst, XAie_BackendType Backend) {
+MIAIE_XAIE_API AieRC XAie_SetIOBackend(XAie_DevInst* DevInst, XAie_BackendType Backend) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   for (const XAie_Backend& b : kBackends)
@@ -587,14 +598,14 @@ MIAIE_XAIE_API AieRC XAie_SetIOBackend(XAie_DevInst* DevInst, XAie_BackendType B
       return XAIE_OK;
     }
   return fail(d, XAIE_INVALID_ARGS, "XAie_SetIOBackend: unknown backend %d", (int)Backend);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_UpdateNpiAddr(XAie_DevInst* DevInst, u64 NpiAddr) {
+MIAIE_XAIE_API AieRC XAie_UpdateNpiAddr(XAie_DevInst* DevInst, u64 NpiAddr) try {
   (void)NpiAddr;
   return dev_of(DevInst) ? XAIE_OK : XAIE_INVALID_DEVICE;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_PartitionInitialize(XAie_DevInst* DevInst, void* Opts) {
+MIAIE_XAIE_API AieRC XAie_PartitionInitialize(XAie_DevInst* DevInst, void* Opts) try {
   (void)Opts;
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
@@ -605,27 +616,27 @@ MIAIE_XAIE_API AieRC XAie_PartitionInitialize(XAie_DevInst* DevInst, void* Opts)
   if (e != hipSuccess) return hip_fail(d, e, "XAie_PartitionInitialize: clearing tile memory");
   reset_state(d);
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_PmRequestTiles(XAie_DevInst* DevInst, XAie_LocType* Loc, u32 NumTiles) {
+MIAIE_XAIE_API AieRC XAie_PmRequestTiles(XAie_DevInst* DevInst, XAie_LocType* Loc, u32 NumTiles) try {
   (void)Loc;
   (void)NumTiles;
   return XAie_PartitionInitialize(DevInst, nullptr);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_PartitionTeardown(XAie_DevInst* DevInst) {
+MIAIE_XAIE_API AieRC XAie_PartitionTeardown(XAie_DevInst* DevInst) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   destroy(d);
   DevInst->Priv = nullptr;
   DevInst->IsReady = 0;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
 MIAIE_XAIE_API AieRC XAie_Finish(XAie_DevInst* DevInst) { return XAie_PartitionTeardown(DevInst); }
 
 // ---------------------------------------------------------------- cores
-MIAIE_XAIE_API AieRC XAie_CoreReset(XAie_DevInst* DevInst, XAie_LocType Loc) {
+MIAIE_XAIE_API AieRC XAie_CoreReset(XAie_DevInst* DevInst, XAie_LocType Loc) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   int t;
@@ -635,18 +646,18 @@ MIAIE_XAIE_API AieRC XAie_CoreReset(XAie_DevInst* DevInst, XAie_LocType Loc) {
   c.reset = true;
   c.enabled = false;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_CoreUnreset(XAie_DevInst* DevInst, XAie_LocType Loc) {
+MIAIE_XAIE_API AieRC XAie_CoreUnreset(XAie_DevInst* DevInst, XAie_LocType Loc) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   int t;
   if (AieRC rc = core_of(d, Loc, "XAie_CoreUnreset", &t)) return rc;
   d->cores[t].reset = false;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_LoadElfMem(XAie_DevInst* DevInst, XAie_LocType Loc, const unsigned char* ElfMem) {
+MIAIE_XAIE_API AieRC XAie_LoadElfMem(XAie_DevInst* DevInst, XAie_LocType Loc, const unsigned char* ElfMem) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   int t;
@@ -661,9 +672,9 @@ MIAIE_XAIE_API AieRC XAie_LoadElfMem(XAie_DevInst* DevInst, XAie_LocType Loc, co
   c.enabled = false;
   c.ran = false;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_CoreEnable(XAie_DevInst* DevInst, XAie_LocType Loc) {
+MIAIE_XAIE_API AieRC XAie_CoreEnable(XAie_DevInst* DevInst, XAie_LocType Loc) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   int t;
@@ -674,9 +685,9 @@ MIAIE_XAIE_API AieRC XAie_CoreEnable(XAie_DevInst* DevInst, XAie_LocType Loc) {
   c.enabled = true;
   c.pending = true;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_CoreDisable(XAie_DevInst* DevInst, XAie_LocType Loc) {
+MIAIE_XAIE_API AieRC XAie_CoreDisable(XAie_DevInst* DevInst, XAie_LocType Loc) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   int t;
@@ -684,9 +695,9 @@ MIAIE_XAIE_API AieRC XAie_CoreDisable(XAie_DevInst* DevInst, XAie_LocType Loc) {
   if (AieRC rc = flush(d)) return rc;
   d->cores[t].enabled = false;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_CoreWaitForDone(XAie_DevInst* DevInst, XAie_LocType Loc, u32 TimeOut) {
+MIAIE_XAIE_API AieRC XAie_CoreWaitForDone(XAie_DevInst* DevInst, XAie_LocType Loc, u32 TimeOut) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   int t;
@@ -701,9 +712,9 @@ MIAIE_XAIE_API AieRC XAie_CoreWaitForDone(XAie_DevInst* DevInst, XAie_LocType Lo
       return fail(d, XAIE_CORE_STATUS_TIMEOUT, "XAie_CoreWaitForDone: tile (%u, %u) not done", Loc.Col, Loc.Row);
     std::this_thread::yield();
   }
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_CoreReadDoneBit(XAie_DevInst* DevInst, XAie_LocType Loc, u8* DoneBit) {
+MIAIE_XAIE_API AieRC XAie_CoreReadDoneBit(XAie_DevInst* DevInst, XAie_LocType Loc, u8* DoneBit) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   if (!DoneBit) return fail(d, XAIE_INVALID_ARGS, "XAie_CoreReadDoneBit: DoneBit is NULL");
@@ -712,9 +723,9 @@ MIAIE_XAIE_API AieRC XAie_CoreReadDoneBit(XAie_DevInst* DevInst, XAie_LocType Lo
   if (AieRC rc = flush(d)) return rc;
   *DoneBit = core_done(d, t) ? 1 : 0;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_CoreGetStatus(XAie_DevInst* DevInst, XAie_LocType Loc, u32* CoreStatus) {
+MIAIE_XAIE_API AieRC XAie_CoreGetStatus(XAie_DevInst* DevInst, XAie_LocType Loc, u32* CoreStatus) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   if (!CoreStatus) return fail(d, XAIE_INVALID_ARGS, "XAie_CoreGetStatus: CoreStatus is NULL");
@@ -730,10 +741,10 @@ MIAIE_XAIE_API AieRC XAie_CoreGetStatus(XAie_DevInst* DevInst, XAie_LocType Loc,
   if (core_done(d, t)) s |= XAIE_CORE_STATUS_DONE_BIT;
   *CoreStatus = s;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
 // ---------------------------------------------------------------- data memory
-MIAIE_XAIE_API AieRC XAie_DataMemBlockWrite(XAie_DevInst* DevInst, XAie_LocType Loc, u64 Addr, const void* Src, u32 Size) {
+MIAIE_XAIE_API AieRC XAie_DataMemBlockWrite(XAie_DevInst* DevInst, XAie_LocType Loc, u64 Addr, const void* Src, u32 Size) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   if (!Src && Size) return fail(d, XAIE_INVALID_ARGS, "XAie_DataMemBlockWrite: Src is NULL");
@@ -742,9 +753,9 @@ MIAIE_XAIE_API AieRC XAie_DataMemBlockWrite(XAie_DevInst* DevInst, XAie_LocType 
   if (AieRC rc = tile_range(d, t, Addr, Size, "XAie_DataMemBlockWrite")) return rc;
   if (AieRC rc = flush(d)) return rc;
   return copy_h2d(d, t, Addr, Src, Size);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_DataMemBlockRead(XAie_DevInst* DevInst, XAie_LocType Loc, u64 Addr, void* Dst, u32 Size) {
+MIAIE_XAIE_API AieRC XAie_DataMemBlockRead(XAie_DevInst* DevInst, XAie_LocType Loc, u64 Addr, void* Dst, u32 Size) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return XAIE_INVALID_DEVICE;
   if (!Dst && Size) return fail(d, XAIE_INVALID_ARGS, "XAie_DataMemBlockRead: Dst is NULL");
@@ -753,19 +764,19 @@ MIAIE_XAIE_API AieRC XAie_DataMemBlockRead(XAie_DevInst* DevInst, XAie_LocType L
   if (AieRC rc = tile_range(d, t, Addr, Size, "XAie_DataMemBlockRead")) return rc;
   if (AieRC rc = flush(d)) return rc;
   return copy_d2h(d, t, Addr, Dst, Size);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_DataMemWrWord(XAie_DevInst* DevInst, XAie_LocType Loc, u64 Addr, u32 Data) {
+MIAIE_XAIE_API AieRC XAie_DataMemWrWord(XAie_DevInst* DevInst, XAie_LocType Loc, u64 Addr, u32 Data) try {
   return XAie_DataMemBlockWrite(DevInst, Loc, Addr, &Data, sizeof Data);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_DataMemRdWord(XAie_DevInst* DevInst, XAie_LocType Loc, u64 Addr, u32* Data) {
+MIAIE_XAIE_API AieRC XAie_DataMemRdWord(XAie_DevInst* DevInst, XAie_LocType Loc, u64 Addr, u32* Data) try {
   if (!Data) return fail(DevInst ? DevInst->Priv : nullptr, XAIE_INVALID_ARGS, "XAie_DataMemRdWord: Data is NULL");
   return XAie_DataMemBlockRead(DevInst, Loc, Addr, Data, sizeof *Data);
-}
+} catch (...) { return out_of_memory(__func__); }
 
 // ---------------------------------------------------------------- DDR
-MIAIE_XAIE_API XAie_MemInst* XAie_MemAllocate(XAie_DevInst* DevInst, u64 Size, XAie_MemCacheProp Cache) {
+MIAIE_XAIE_API XAie_MemInst* XAie_MemAllocate(XAie_DevInst* DevInst, u64 Size, XAie_MemCacheProp Cache) try {
   (void)Cache;
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return nullptr;
@@ -794,9 +805,9 @@ MIAIE_XAIE_API XAie_MemInst* XAie_MemAllocate(XAie_DevInst* DevInst, u64 Size, X
   }
   d->ddr.push_back(m);
   return m;
-}
+} catch (...) { out_of_memory(__func__); return nullptr; }
 
-MIAIE_XAIE_API AieRC XAie_MemFree(XAie_MemInst* MemInst) {
+MIAIE_XAIE_API AieRC XAie_MemFree(XAie_MemInst* MemInst) try {
   if (!MemInst) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_MemFree: NULL");
   miaie_xaie_dev* d = MemInst->dev;
   for (size_t i = 0; i < d->ddr.size(); ++i)
@@ -806,32 +817,32 @@ MIAIE_XAIE_API AieRC XAie_MemFree(XAie_MemInst* MemInst) {
       return XAIE_OK;
     }
   return fail(d, XAIE_INVALID_ARGS, "XAie_MemFree: unknown buffer");
-}
+} catch (...) { return out_of_memory(__func__); }
 
 MIAIE_XAIE_API void* XAie_MemGetVAddr(XAie_MemInst* MemInst) { return MemInst ? MemInst->host : nullptr; }
 
-MIAIE_XAIE_API u64 XAie_MemGetDevAddr(XAie_MemInst* MemInst) {
+MIAIE_XAIE_API u64 XAie_MemGetDevAddr(XAie_MemInst* MemInst) try {
   return MemInst ? (u64) reinterpret_cast<uintptr_t>(MemInst->host) : 0;
-}
+} catch (...) { out_of_memory(__func__); return 0; }
 
-MIAIE_XAIE_API AieRC XAie_MemSyncForDev(XAie_MemInst* MemInst) {
+MIAIE_XAIE_API AieRC XAie_MemSyncForDev(XAie_MemInst* MemInst) try {
   return MemInst ? XAIE_OK : fail(nullptr, XAIE_INVALID_ARGS, "XAie_MemSyncForDev: NULL");
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_MemSyncForCPU(XAie_MemInst* MemInst) {
+MIAIE_XAIE_API AieRC XAie_MemSyncForCPU(XAie_MemInst* MemInst) try {
   return MemInst ? XAIE_OK : fail(nullptr, XAIE_INVALID_ARGS, "XAie_MemSyncForCPU: NULL");
-}
+} catch (...) { return out_of_memory(__func__); }
 
 // ---------------------------------------------------------------- routing and moves
-MIAIE_XAIE_API XAie_RoutingInstance* XAie_InitRoutingHandler(XAie_DevInst* DevInst) {
+MIAIE_XAIE_API XAie_RoutingInstance* XAie_InitRoutingHandler(XAie_DevInst* DevInst) try {
   miaie_xaie_dev* d = dev_of(DevInst);
   if (!d) return nullptr;
   XAie_RoutingInstance* r = new XAie_RoutingInstance{DevInst, {}};
   d->routing.push_back(r);
   return r;
-}
+} catch (...) { out_of_memory(__func__); return nullptr; }
 
-MIAIE_XAIE_API AieRC XAie_RoutingInstanceFree(XAie_RoutingInstance* ri) {
+MIAIE_XAIE_API AieRC XAie_RoutingInstanceFree(XAie_RoutingInstance* ri) try {
   if (!ri) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_RoutingInstanceFree: NULL");
   miaie_xaie_dev* d = dev_of(ri->dev);
   if (!d) return XAIE_INVALID_DEVICE;
@@ -842,10 +853,10 @@ MIAIE_XAIE_API AieRC XAie_RoutingInstanceFree(XAie_RoutingInstance* ri) {
       return XAIE_OK;
     }
   return fail(d, XAIE_INVALID_ARGS, "XAie_RoutingInstanceFree: unknown routing instance");
-}
+} catch (...) { return out_of_memory(__func__); }
 
 MIAIE_XAIE_API AieRC XAie_Route(XAie_RoutingInstance* ri, void* RouteConstraints, XAie_LocType Source,
-                                XAie_LocType Destination) {
+                                XAie_LocType Destination) try {
   (void)RouteConstraints;
   if (!ri) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_Route: routing instance is NULL");
   miaie_xaie_dev* d = dev_of(ri->dev);
@@ -860,10 +871,10 @@ MIAIE_XAIE_API AieRC XAie_Route(XAie_RoutingInstance* ri, void* RouteConstraints
                 Destination.Col, Destination.Row);
   if (!has_route(ri, s, t)) ri->routes.push_back(Route{(u16)s, (u16)t});
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
 MIAIE_XAIE_API AieRC XAie_MoveData(XAie_RoutingInstance* ri, XAie_LocType Source, void* SrcAddr, u32 Size,
-                                   void* DstAddr, XAie_LocType Destination) {
+                                   void* DstAddr, XAie_LocType Destination) try {
   if (!ri) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_MoveData: routing instance is NULL");
   miaie_xaie_dev* d = dev_of(ri->dev);
   if (!d) return XAIE_INVALID_DEVICE;
@@ -894,10 +905,10 @@ MIAIE_XAIE_API AieRC XAie_MoveData(XAie_RoutingInstance* ri, XAie_LocType Source
   if (Size == 0) return XAIE_OK;
   const int rc = miaie_copy_d2d(d->ctx, d->mem + d->off[t] + dst, d->mem + d->off[s] + src, Size);
   return rc ? miaie_fail(d, rc, "XAie_MoveData: tile to tile copy") : XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
 MIAIE_XAIE_API AieRC XAie_MoveDataExternal2Aie(XAie_RoutingInstance* ri, XAie_LocType Source, XAie_MemInst* MemInst,
-                                               u32 Size, u64 DstAddr, XAie_LocType Destination) {
+                                               u32 Size, u64 DstAddr, XAie_LocType Destination) try {
   if (!MemInst) return fail(ri && ri->dev ? ri->dev->Priv : nullptr, XAIE_INVALID_ARGS, "XAie_MoveDataExternal2Aie: MemInst is NULL");
   if (Size > MemInst->size)
     return fail(MemInst->dev, XAIE_INVALID_ARGS, "XAie_MoveDataExternal2Aie: %u B from a %zu B buffer", Size, MemInst->size);
@@ -905,10 +916,10 @@ MIAIE_XAIE_API AieRC XAie_MoveDataExternal2Aie(XAie_RoutingInstance* ri, XAie_Lo
     return fail(MemInst->dev, XAIE_INVALID_TILE, "XAie_MoveDataExternal2Aie: source (%u, %u) is not a shim tile",
                 Source.Col, Source.Row);
   return XAie_MoveData(ri, Source, MemInst->host, Size, reinterpret_cast<void*>((uintptr_t)DstAddr), Destination);
-}
+} catch (...) { return out_of_memory(__func__); }
 
 MIAIE_XAIE_API AieRC XAie_MoveDataAie2External(XAie_RoutingInstance* ri, XAie_LocType Source, u64 SrcAddr, u32 Size,
-                                               XAie_MemInst* MemInst, XAie_LocType Destination) {
+                                               XAie_MemInst* MemInst, XAie_LocType Destination) try {
   if (!MemInst) return fail(ri && ri->dev ? ri->dev->Priv : nullptr, XAIE_INVALID_ARGS, "XAie_MoveDataAie2External: MemInst is NULL");
   if (Size > MemInst->size)
     return fail(MemInst->dev, XAIE_INVALID_ARGS, "XAie_MoveDataAie2External: %u B into a %zu B buffer", Size, MemInst->size);
@@ -917,9 +928,9 @@ MIAIE_XAIE_API AieRC XAie_MoveDataAie2External(XAie_RoutingInstance* ri, XAie_Lo
     return fail(MemInst->dev, XAIE_INVALID_TILE, "XAie_MoveDataAie2External: destination (%u, %u) is not a shim tile",
                 Destination.Col, Destination.Row);
   return XAie_MoveData(ri, Source, reinterpret_cast<void*>((uintptr_t)SrcAddr), Size, MemInst->host, Destination);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_RouteDmaWait(XAie_RoutingInstance* ri, XAie_LocType Source, XAie_LocType Destination, u8 IsMm2s) {
+MIAIE_XAIE_API AieRC XAie_RouteDmaWait(XAie_RoutingInstance* ri, XAie_LocType Source, XAie_LocType Destination, u8 IsMm2s) try {
   (void)IsMm2s;
   if (!ri) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_RouteDmaWait: routing instance is NULL");
   miaie_xaie_dev* d = dev_of(ri->dev);
@@ -929,9 +940,9 @@ MIAIE_XAIE_API AieRC XAie_RouteDmaWait(XAie_RoutingInstance* ri, XAie_LocType So
     return fail(d, XAIE_ERR_NO_ROUTE, "XAie_RouteDmaWait: no route (%u, %u) -> (%u, %u)", Source.Col, Source.Row,
                 Destination.Col, Destination.Row);
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_Run(XAie_RoutingInstance* ri, u32 Iterations) {
+MIAIE_XAIE_API AieRC XAie_Run(XAie_RoutingInstance* ri, u32 Iterations) try {
   if (!ri) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_Run: routing instance is NULL");
   miaie_xaie_dev* d = dev_of(ri->dev);
   if (!d) return XAIE_INVALID_DEVICE;
@@ -950,7 +961,7 @@ MIAIE_XAIE_API AieRC XAie_Run(XAie_RoutingInstance* ri, u32 Iterations) {
   }
   if (tiles.empty()) return fail(d, XAIE_ERR, "XAie_Run: no loaded, out-of-reset core on this instance's routes");
   return launch_cores(d, tiles, Iterations);
-}
+} catch (...) { return out_of_memory(__func__); }
 
 }  // extern "C"
 
@@ -991,7 +1002,7 @@ const XAie_MiaieKernel* builtin_by_name(const char* name) {
 
 extern "C" {
 
-MIAIE_XAIE_API XAie_Kernel_Inst* XAie_LoadKernel(const char* Name, int Col, int Row) {
+MIAIE_XAIE_API XAie_Kernel_Inst* XAie_LoadKernel(const char* Name, int Col, int Row) try {
   if (!Name) {
     fail(nullptr, XAIE_INVALID_ARGS, "XAie_LoadKernel: Name is NULL");
     return nullptr;
@@ -1015,23 +1026,23 @@ MIAIE_XAIE_API XAie_Kernel_Inst* XAie_LoadKernel(const char* Name, int Col, int 
   if (!ri) return nullptr;
   g_implicit.refs++;
   return new XAie_Kernel_Inst{loc, k, ri};
-}
+} catch (...) { out_of_memory(__func__); return nullptr; }
 
-MIAIE_XAIE_API AieRC XAie_RoutingHostToAie(XAie_Kernel_Inst* K, XAie_LocType Shim) {
+MIAIE_XAIE_API AieRC XAie_RoutingHostToAie(XAie_Kernel_Inst* K, XAie_LocType Shim) try {
   if (!K) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_RoutingHostToAie: kernel is NULL");
   if (AieRC rc = XAie_Route(K->ri, nullptr, Shim, K->loc)) return rc;
   K->shim_in = tile_index(g_implicit.inst.Priv, Shim);
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_RoutingAieToHost(XAie_Kernel_Inst* K, XAie_LocType Shim) {
+MIAIE_XAIE_API AieRC XAie_RoutingAieToHost(XAie_Kernel_Inst* K, XAie_LocType Shim) try {
   if (!K) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_RoutingAieToHost: kernel is NULL");
   if (AieRC rc = XAie_Route(K->ri, nullptr, K->loc, Shim)) return rc;
   K->shim_out = tile_index(g_implicit.inst.Priv, Shim);
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_MoveDataToAie(XAie_Kernel_Inst* K, int Input, const void* Src, size_t Bytes) {
+MIAIE_XAIE_API AieRC XAie_MoveDataToAie(XAie_Kernel_Inst* K, int Input, const void* Src, size_t Bytes) try {
   if (!K || !Src) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_MoveDataToAie: NULL argument");
   miaie_xaie_dev* d = dev_of(&g_implicit.inst);
   if (!d) return XAIE_INVALID_DEVICE;
@@ -1052,9 +1063,9 @@ MIAIE_XAIE_API AieRC XAie_MoveDataToAie(XAie_Kernel_Inst* K, int Input, const vo
   if (AieRC rc = tile_range(d, t, ping[0], Bytes, "XAie_MoveDataToAie")) return rc;
   if (AieRC rc = flush(d)) return rc;
   return copy_h2d(d, t, ping[0], Src, Bytes);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_RunCore(XAie_Kernel_Inst* K) {
+MIAIE_XAIE_API AieRC XAie_RunCore(XAie_Kernel_Inst* K) try {
   if (!K) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_RunCore: kernel is NULL");
   miaie_xaie_dev* d = dev_of(&g_implicit.inst);
   if (!d) return XAIE_INVALID_DEVICE;
@@ -1062,9 +1073,9 @@ MIAIE_XAIE_API AieRC XAie_RunCore(XAie_Kernel_Inst* K) {
   if (AieRC rc = flush(d)) return rc;
   d->cores[t].enabled = true;
   return launch_cores(d, std::vector<int>{t}, 1);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_WaitOutData(XAie_Kernel_Inst* K) {
+MIAIE_XAIE_API AieRC XAie_WaitOutData(XAie_Kernel_Inst* K) try {
   if (!K) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_WaitOutData: kernel is NULL");
   miaie_xaie_dev* d = dev_of(&g_implicit.inst);
   if (!d) return XAIE_INVALID_DEVICE;
@@ -1074,9 +1085,9 @@ MIAIE_XAIE_API AieRC XAie_WaitOutData(XAie_Kernel_Inst* K) {
   if (miaie_wait(d->ctx, -1)) return miaie_fail(d, MIAIE_EHIP, "XAie_WaitOutData");
   retire(d);
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_MoveAieToData(XAie_Kernel_Inst* K, int Output, void* Dst, size_t Bytes) {
+MIAIE_XAIE_API AieRC XAie_MoveAieToData(XAie_Kernel_Inst* K, int Output, void* Dst, size_t Bytes) try {
   if (!K || !Dst) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_MoveAieToData: NULL argument");
   miaie_xaie_dev* d = dev_of(&g_implicit.inst);
   if (!d) return XAIE_INVALID_DEVICE;
@@ -1088,21 +1099,21 @@ MIAIE_XAIE_API AieRC XAie_MoveAieToData(XAie_Kernel_Inst* K, int Output, void* D
   if (AieRC rc = tile_range(d, t, ping[1], Bytes, "XAie_MoveAieToData")) return rc;
   if (AieRC rc = flush(d)) return rc;
   return copy_d2h(d, t, ping[1], Dst, Bytes);
-}
+} catch (...) { return out_of_memory(__func__); }
 
-MIAIE_XAIE_API AieRC XAie_KernelFree(XAie_Kernel_Inst* K) {
+MIAIE_XAIE_API AieRC XAie_KernelFree(XAie_Kernel_Inst* K) try {
   if (!K) return fail(nullptr, XAIE_INVALID_ARGS, "XAie_KernelFree: NULL");
   XAie_RoutingInstanceFree(K->ri);
   delete K;
   if (--g_implicit.refs == 0) return XAie_PartitionTeardown(&g_implicit.inst);
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
 
 }  // extern "C"
 
 // ======================================================================== launches on DDR addresses
 extern "C" MIAIE_XAIE_API AieRC XAie_MiaieRunOnDdr(const XAie_MiaieKernel* Kernel, u32 Cols, u32 Rows, u32 ColStart,
-                                                   u32 RowStart, u64 InAddr, u64 OutAddr) {
+                                                   u32 RowStart, u64 InAddr, u64 OutAddr) try {
   const XAie_MiaieKernel* k = nullptr;
   if (AieRC rc = valid_kernel(nullptr, Kernel, &k)) return rc;
   if (k->NumParams != 2) return fail(nullptr, XAIE_NOT_SUPPORTED, "XAie_MiaieRunOnDdr: kernel %s has %u windows, not 2",
@@ -1159,4 +1170,4 @@ extern "C" MIAIE_XAIE_API AieRC XAie_MiaieRunOnDdr(const XAie_MiaieKernel* Kerne
     if (AieRC rc = copy_d2h(d, tiles[i], ping[1], reinterpret_cast<void*>((uintptr_t)OutAddr + i * out_bytes), out_bytes))
       return rc;
   return XAIE_OK;
-}
+} catch (...) { return out_of_memory(__func__); }
