@@ -109,6 +109,22 @@ def timed(ctx, timer, fn, steps: int, warmup: int) -> float:
     return ms / steps
 
 
+def single_launch_us(ctx, timer, fn, reps: int, flush=None) -> float:
+    """Median over `reps` single launches, each alone between its own pair of
+    events on a drained stream.  With `flush`, that call runs first (outside
+    the events) so the launch starts from cold caches."""
+    ts = []
+    for _ in range(reps):
+        if flush is not None:
+            flush()
+        ctx.wait(120_000)
+        timer.start()
+        fn()
+        ts.append(timer.stop_ms() * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
 def read_traffic() -> tuple[int | None, str | None]:
     """HBM bytes per launch recorded in the committed rocprofv3 summary."""
     if not os.path.exists(TRAFFIC_FILE):
@@ -341,6 +357,15 @@ def main() -> int:
         ctx.fill_i8(dW, Co * 9 * Ci, 4)
         ms_c = timed(ctx, timer, lambda: ctx.conv2d_i8_nhwc(dX, dW, dS, dYc, Nb, H, W, Ci, Co, 3, 3, 1, 1),
                      max(args.steps, 200), args.warmup)
+        # single launches, hot and cold: "cold" writes 512 MiB first (twice the
+        # 256 MB MALL; the L2s start every kernel invalidated anyway), so the
+        # convolution reads X and W from HBM
+        conv1 = lambda: ctx.conv2d_i8_nhwc(dX, dW, dS, dYc, Nb, H, W, Ci, Co, 3, 3, 1, 1)
+        flush_bytes = 512 << 20
+        dF = ctx.alloc(flush_bytes)
+        us_hot1 = single_launch_us(ctx, timer, conv1, 50)
+        us_cold1 = single_launch_us(ctx, timer, conv1, 50, lambda: ctx.fill_i8(dF, flush_bytes, 11))
+        dF.free()
         # the same convolution recorded 20 times into one graph (miaie_graph_*):
         # replays have no host launch gap between the convolutions
         chain = 20
@@ -363,6 +388,9 @@ def main() -> int:
             "graph_chain": {"convs_per_replay": chain, "us_per_conv": round(ms_cg * 1e3, 3),
                             "gops": round(conv_ops / (ms_cg * 1e-3) / 1e9, 1),
                             "frac": round(conv_ops / (ms_cg * 1e-3) / 1e12 / roof, 4)},
+            "single_launch_us": {"hot": round(us_hot1, 3), "cold_hbm": round(us_cold1, 3),
+                                 "how": "median of 50 launches, each alone between two events on a drained stream; "
+                                        "cold_hbm writes 512 MiB before each launch (outside the events)"},
             "note": "events bracket back-to-back launches, so us_per_step includes the gap between launches; "
                     "graph_chain replays 20 recorded convolutions per launch",
         }
