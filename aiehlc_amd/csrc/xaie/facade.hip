@@ -185,6 +185,9 @@ struct miaie_xaie_dev {
   std::deque<std::pair<uint64_t, hipEvent_t>> inflight;  // launch batches not yet seen complete
   std::vector<hipEvent_t> spare;
   uint64_t issued = 0, completed = 0;
+  uint8_t* stage = nullptr;        // pinned host staging for host <-> tile copies
+  size_t stage_used = 0;           // bytes of it taken since the stream last drained
+  hipEvent_t stage_ev = nullptr;   // recorded after the latest staged host -> tile copy
   XAie_BackendType backend = XAIE_IO_BACKEND_BAREMETAL;
   std::string err;
 };
@@ -427,16 +430,82 @@ AieRC tile_range(miaie_xaie_dev* d, int t, uint64_t addr, uint64_t size, const c
   return XAIE_OK;
 }
 
+// Host <-> tile copies up to kStageBytes go through a pinned staging buffer.
+// A host -> tile copy returns once the source bytes are in the staging
+// buffer; the device copy then runs in stream order, ahead of any later
+// launch or copy, as an AIE DMA runs on after XAie_MoveData returns (the
+// perf example waits for it with XAie_RouteDmaWait, aieml_perf.cc:156-163).
+// A tile -> host copy returns once the bytes are in the destination.  Larger
+// copies take the synchronous miaie copies.  Staged host -> tile copies take
+// consecutive slices of the buffer; when it is full, the copies still reading
+// it are waited for and it starts over.
+constexpr size_t kStageBytes = 4u << 20;
+
+AieRC stage_take(miaie_xaie_dev* d, size_t size, uint8_t** slice) {
+  hipError_t e = hipSetDevice(d->device);
+  if (e != hipSuccess) return hip_fail(d, e, "hipSetDevice");
+  if (!d->stage) {
+    e = hipHostMalloc(reinterpret_cast<void**>(&d->stage), kStageBytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      d->stage = nullptr;
+      return hip_fail(d, e, "pinned staging buffer");
+    }
+    d->stage_used = 0;
+  }
+  if (!d->stage_ev) {
+    e = hipEventCreateWithFlags(&d->stage_ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      d->stage_ev = nullptr;
+      return hip_fail(d, e, "hipEventCreate");
+    }
+  }
+  const size_t need = (size + 255) & ~static_cast<size_t>(255);
+  if (d->stage_used + need > kStageBytes) {
+    e = hipEventSynchronize(d->stage_ev);
+    if (e != hipSuccess) return hip_fail(d, e, "waiting for staged copies");
+    d->stage_used = 0;
+  }
+  *slice = d->stage + d->stage_used;
+  d->stage_used += need;
+  return XAIE_OK;
+}
+
 AieRC copy_h2d(miaie_xaie_dev* d, int t, uint64_t addr, const void* src, size_t size) {
   if (size == 0) return XAIE_OK;
+  if (size <= kStageBytes) {
+    uint8_t* st = nullptr;
+    if (AieRC rc = stage_take(d, size, &st)) return rc;
+    std::memcpy(st, src, size);
+    hipError_t e = hipMemcpyAsync(d->mem + d->off[t] + addr, st, size, hipMemcpyHostToDevice, d->stream);
+    if (e == hipSuccess) e = hipEventRecord(d->stage_ev, d->stream);
+    return e == hipSuccess ? XAIE_OK : hip_fail(d, e, "host to tile copy");
+  }
   const int rc = miaie_copy_h2d(d->ctx, d->mem + d->off[t] + addr, src, size);
   return rc ? miaie_fail(d, rc, "host to tile copy") : XAIE_OK;
 }
 
 AieRC copy_d2h(miaie_xaie_dev* d, int t, uint64_t addr, void* dst, size_t size) {
   if (size == 0) return XAIE_OK;
+  if (size <= kStageBytes) {
+    uint8_t* st = nullptr;
+    if (AieRC rc = stage_take(d, size, &st)) return rc;
+    hipError_t e = hipMemcpyAsync(st, d->mem + d->off[t] + addr, size, hipMemcpyDeviceToHost, d->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) return hip_fail(d, e, "tile to host copy");
+    std::memcpy(dst, st, size);
+    d->stage_used = 0;  // the stream has drained: no copy reads the buffer any more
+    return XAIE_OK;
+  }
   const int rc = miaie_copy_d2h(d->ctx, dst, d->mem + d->off[t] + addr, size);
   return rc ? miaie_fail(d, rc, "tile to host copy") : XAIE_OK;
+}
+
+// Waits until every staged host -> tile copy has landed.
+AieRC staged_copies_done(miaie_xaie_dev* d) {
+  if (!d->stage_ev) return XAIE_OK;
+  hipError_t e = hipSetDevice(d->device);
+  if (e == hipSuccess) e = hipEventSynchronize(d->stage_ev);
+  return e == hipSuccess ? XAIE_OK : hip_fail(d, e, "waiting for staged copies");
 }
 
 void free_ddr(XAie_MemInst* m) {
@@ -455,6 +524,8 @@ void destroy(miaie_xaie_dev* d) {
   for (hipEvent_t e : d->spare) (void)hipEventDestroy(e);
   for (XAie_MemInst* m : d->ddr) free_ddr(m);
   for (XAie_RoutingInstance* r : d->routing) delete r;
+  if (d->stage) (void)hipHostFree(d->stage);
+  if (d->stage_ev) (void)hipEventDestroy(d->stage_ev);
   if (d->mem) miaie_free(d->ctx, d->mem);
   if (d->ctx) miaie_finish(d->ctx);
   delete d;
@@ -939,7 +1010,7 @@ MIAIE_XAIE_API AieRC XAie_RouteDmaWait(XAie_RoutingInstance* ri, XAie_LocType So
   if (s < 0 || t < 0 || !has_route(ri, s, t))
     return fail(d, XAIE_ERR_NO_ROUTE, "XAie_RouteDmaWait: no route (%u, %u) -> (%u, %u)", Source.Col, Source.Row,
                 Destination.Col, Destination.Row);
-  return XAIE_OK;
+  return staged_copies_done(d);
 } catch (...) { return out_of_memory(__func__); }
 
 MIAIE_XAIE_API AieRC XAie_Run(XAie_RoutingInstance* ri, u32 Iterations) try {

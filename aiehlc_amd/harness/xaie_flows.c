@@ -5,18 +5,21 @@
  * Each subcommand follows one example's sequence of XAie_* calls and checks
  * the result the way that example does (CPU golden or its constant), then
  * exits 0 on a match:
- *   mm            example/matrixmultiply/aieml_mm.cc:108-249 (+ main :251-296)
- *   perf          example/perf/aieml_perf.cc:105-254, partitioned at column 2
+ *   mm [reps]     example/matrixmultiply/aieml_mm.cc:108-249 (+ main :251-296),
+ *                 timed over the span aieml_mm.cc:148-190 times
+ *   perf [reps]   example/perf/aieml_perf.cc:105-254, partitioned at column 2
  *   multi_tile    example/multi/multi_tile.cpp:65-181 (expects 26)
  *   seq_full_col  example/multi/seq_full_col.cpp:65-181 (expects 23)
  *   vek385 [cols] example/multi/vek385_verification.cpp:72-230 (expects 3*v^2)
  *   oob           example/other/aieoob.c:76-150 (kernel-instance calls, 8x8)
  *   errors        argument and routing errors the facade must reject
  */
+#define _POSIX_C_SOURCE 199309L /* clock_gettime */
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "miaie_xaie.h"
 
@@ -73,6 +76,17 @@ static int golden_mismatches(const int32_t* in, const int32_t* out, int n) {
   return bad;
 }
 
+static double now_us(void) {
+  struct timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return t.tv_sec * 1e6 + t.tv_nsec * 1e-3;
+}
+
+static int cmp_double(const void* a, const void* b) {
+  const double x = *(const double*)a, y = *(const double*)b;
+  return (x > y) - (x < y);
+}
+
 /* Wait for one core the way the examples do: poll until XAIE_OK
  * (aieml_mm.cc:172-182), here with an upper bound so a failure ends. */
 static void wait_core(XAie_DevInst* dev, XAie_LocType loc) {
@@ -85,7 +99,7 @@ static void wait_core(XAie_DevInst* dev, XAie_LocType loc) {
 
 /* aieml_mm.cc / aieml_perf.cc: one 16x16 NT tile through DDR -> tile -> DDR. */
 static int flow_window(const XAie_MiaieKernel* kernel, int startcol, int ncols, int shimcol, int first_value,
-                       int use_ext_calls) {
+                       int use_ext_calls, int reps) {
   enum { N = 16, MAT_SIZE = N * N };
   XAie_DevInst dev;
   open_device(&dev, startcol, ncols);
@@ -114,19 +128,35 @@ static int flow_window(const XAie_MiaieKernel* kernel, int startcol, int ncols, 
   CHECK(XAie_MemSyncForDev(out));
 
   const u32 CORE_IP_MEM = 0x1000, CORE_OP_MEM = 0x6000;
-  if (use_ext_calls)
-    CHECK(XAie_MoveDataExternal2Aie(ri, shim, in, mlen * sizeof(u32), CORE_IP_MEM, core));
-  else
-    CHECK(XAie_MoveData(ri, shim, (void*)(uintptr_t)phy, mlen * sizeof(u32), (void*)(uintptr_t)CORE_IP_MEM, core));
-  CHECK(XAie_RouteDmaWait(ri, shim, core, 1));
-  CHECK(XAie_Run(ri, 1));
-  wait_core(&dev, core);
-  if (use_ext_calls)
-    CHECK(XAie_MoveDataAie2External(ri, core, CORE_OP_MEM, mlen * sizeof(u32), out, shim));
-  else
-    CHECK(XAie_MoveData(ri, core, (void*)(uintptr_t)CORE_OP_MEM, recv_len * sizeof(u32), (void*)(uintptr_t)phy_out,
-                        shim));
-  CHECK(XAie_MemSyncForCPU(out));
+  /* The stopwatch spans what aieml_mm.cc:148-190 times: the move into the
+   * tile, the run, the wait, the move back and MemSyncForCPU.  With reps > 1
+   * the same sequence repeats and the median is printed as well. */
+  double* us = (double*)calloc((size_t)reps, sizeof(double));
+  if (!us) return 1;
+  for (int r = 0; r < reps; r++) {
+    const double t0 = now_us();
+    if (use_ext_calls) {
+      CHECK(XAie_MoveDataExternal2Aie(ri, shim, in, mlen * sizeof(u32), CORE_IP_MEM, core));
+      CHECK(XAie_RouteDmaWait(ri, shim, core, 1));
+    } else {
+      CHECK(XAie_MoveData(ri, shim, (void*)(uintptr_t)phy, mlen * sizeof(u32), (void*)(uintptr_t)CORE_IP_MEM, core));
+    }
+    CHECK(XAie_Run(ri, 1));
+    wait_core(&dev, core);
+    if (use_ext_calls)
+      CHECK(XAie_MoveDataAie2External(ri, core, CORE_OP_MEM, mlen * sizeof(u32), out, shim));
+    else
+      CHECK(XAie_MoveData(ri, core, (void*)(uintptr_t)CORE_OP_MEM, recv_len * sizeof(u32), (void*)(uintptr_t)phy_out,
+                          shim));
+    CHECK(XAie_MemSyncForCPU(out));
+    us[r] = now_us() - t0;
+  }
+  printf("Output took %.2f us.\n", us[0]);
+  if (reps > 1) {
+    qsort(us, (size_t)reps, sizeof(double), cmp_double);
+    printf("median over %d runs: %.2f us (min %.2f us)\n", reps, us[reps / 2], us[0]);
+  }
+  free(us);
 
   const int bad = golden_mismatches((const int32_t*)XAie_MemGetVAddr(in), (const int32_t*)XAie_MemGetVAddr(out), N);
   const int32_t* o = (const int32_t*)XAie_MemGetVAddr(out);
@@ -386,12 +416,16 @@ static int flow_errors(void) {
 
 int main(int argc, char** argv) {
   if (argc < 2) {
-    fprintf(stderr, "usage: %s mm|perf|multi_tile|seq_full_col|vek385 [cols]|oob|errors\n", argv[0]);
+    fprintf(stderr, "usage: %s mm [reps]|perf [reps]|multi_tile|seq_full_col|vek385 [cols]|oob|errors\n", argv[0]);
     return 64;
   }
   const char* cmd = argv[1];
-  if (!strcmp(cmd, "mm")) return flow_window(&miaie_xaie_mm, 0, 0, 2, 0, 0);       /* aieml_mm.cc:137-140 */
-  if (!strcmp(cmd, "perf")) return flow_window(&miaie_xaie_perf, 2, 34, 33, 1, 1); /* aieml_perf.cc:141-144 */
+  const int reps = argc > 2 ? atoi(argv[2]) : 1;
+  if (!strcmp(cmd, "mm") || !strcmp(cmd, "perf")) {
+    if (reps < 1 || reps > 100000) return 64;
+    if (!strcmp(cmd, "mm")) return flow_window(&miaie_xaie_mm, 0, 0, 2, 0, 0, reps);   /* aieml_mm.cc:137-140 */
+    return flow_window(&miaie_xaie_perf, 2, 34, 33, 1, 1, reps);                      /* aieml_perf.cc:141-144 */
+  }
   if (!strcmp(cmd, "multi_tile")) return flow_multi_tile();
   if (!strcmp(cmd, "seq_full_col")) return flow_seq_full_col();
   if (!strcmp(cmd, "vek385")) {

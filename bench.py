@@ -19,6 +19,10 @@ Also in the line (not the headline):
                          conv's and the GEMM's grid and LDS size
                          (aiehlc_amd/probes/launch_floor); the conv line carries
                          its own floor and the time above it
+  extras.reference_flow_16x16  the reference's own timed example flow
+                         (aieml_mm.cc: 16x16 int32 tile moved in, run, waited
+                         for, moved out) through the aie-rt facade, beside the
+                         215 us the reference prints for it
   extras.vendor_library  the same int8 4096^3 and bf16 8192^3 products through
                          hipBLASLt (torch._int_mm / torch.matmul) on this GPU
   cpu_baseline           the reference's CPU golden loop (i-j-k, int32
@@ -52,6 +56,7 @@ PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_rq_4096_traffic.txt")
 CEILING_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "mfma_ceiling")
 FLOOR_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "launch_floor")
+FLOWS_EXE = os.path.join(ROOT, "aiehlc_amd", "harness", "xaie_flows")
 METRIC = "int8 GEMM TOPS (% MFMA peak) at 4096^3; int8 conv2d 3x3 GOPS; vs host CPU"
 
 
@@ -252,6 +257,29 @@ def mfma_ceiling() -> dict | None:
     return probe_json(CEILING_EXE)
 
 
+def reference_flow(reps: int = 500) -> dict | None:
+    """The reference's own timed example: aieml_mm.cc's XAie_* sequence
+    (move A||B into the tile, run, wait for done, move C out, MemSyncForCPU;
+    the span its stopwatch covers, :148-190) for the 16x16 int32 NT tile,
+    through the aie-rt facade on this GPU.  The reference prints that this
+    span "should be 215 us" for 16x16 on its AIE-ML board (aieml_mm.cc:257)."""
+    if not os.path.exists(FLOWS_EXE):
+        return None
+    r = subprocess.run([FLOWS_EXE, "mm", str(reps)], capture_output=True, text=True, timeout=120)
+    m = re.search(r"median over (\d+) runs: ([0-9.]+) us \(min ([0-9.]+) us\)", r.stdout)
+    first = re.search(r"Output took ([0-9.]+) us", r.stdout)
+    if r.returncode != 0 or not m:
+        return {"error": (r.stdout + r.stderr).strip()[-300:]}
+    med = float(m.group(2))
+    return {"flow": "aieml_mm.cc 16x16 int32 NT: XAie_MoveData in, XAie_Run, XAie_CoreWaitForDone, XAie_MoveData out, "
+                    "XAie_MemSyncForCPU (aiehlc_amd/harness/xaie_flows mm)",
+            "median_us": med, "min_us": float(m.group(3)), "first_us": float(first.group(1)) if first else None,
+            "runs": int(m.group(1)),
+            "reference_expected_us": 215.0,
+            "reference_expected_source": "aieml_mm.cc:257 (printed expectation on VEK280 AIE-ML with caches on)",
+            "speedup_vs_reference_expected": round(215.0 / med, 2)}
+
+
 def vendor_library(steps: int) -> dict:
     """The same GEMMs through ROCm's libraries (hipBLASLt behind torch), on
     the same GPU in the same process: the bar a tuned vendor kernel sets
@@ -443,6 +471,7 @@ def main() -> int:
     ctx.close()
     if not args.no_extras:
         extras["mfma_ceiling"] = mfma_ceiling()
+        extras["reference_flow_16x16"] = reference_flow()
         floor = probe_json(FLOOR_EXE)
         extras["launch_floor"] = floor
         conv = extras.get("conv2d_3x3")

@@ -119,7 +119,9 @@ def test_harness_usage_without_arguments():
 FLOWS = [
     # (args, lines the output must hold): the known answers are the reference's own
     (["mm"], ["C[0][0] = 31960, C[15][15] = 1994200", "CPU result matches"]),     # aieml_mm.cc:137-140
+    (["mm", "50"], ["C[0][0] = 31960, C[15][15] = 1994200", "CPU result matches", "median over 50 runs"]),
     (["perf"], ["C[0][0] = 36312, C[15][15] = 2006232", "CPU result matches"]),   # aieml_perf.cc:141-144
+    (["perf", "20"], ["C[0][0] = 36312, C[15][15] = 2006232", "CPU result matches", "median over 20 runs"]),
     (["multi_tile"], ["out[0] = 26 (expected 26), 0 mismatches"]),                # multi_tile.cpp:150
     (["seq_full_col"], ["rows 3..10", "out[0] = 23 (expected 23), 0 mismatches"]),  # seq_full_col.cpp:163
     (["vek385", "38"], ["38 columns x 4 rows: 0 columns failed, 152 cores executing", "out[0] = 108, iterations = 1024"]),
