@@ -10,8 +10,9 @@ aiehlc_amd/probes/.  Runs on a machine without a GPU
 (hipcc cross-compiles).
 
 Flags: -O3, C++17, hidden visibility (only the MIAIE_API symbols of
-include/miaie.h are exported), and packed-FP32 instruction selection turned
-off (`-Xclang -target-feature -Xclang -packed-fp32-ops`).
+include/miaie.h are exported), packed-FP32 instruction selection turned
+off (`-Xclang -target-feature -Xclang -packed-fp32-ops`), and kernel
+arguments preloaded into SGPRs (`-mllvm -amdgpu-kernarg-preload-count=16`).
 """
 from __future__ import annotations
 
@@ -35,6 +36,9 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # kernel arguments arrive in SGPRs at wave launch instead of through a
+    # scalar load from the (cold) kernarg segment on each kernel's critical path
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-function",
     f"-I{os.path.join(ROOT, 'include')}",
 ]

@@ -146,88 +146,115 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
   *reinterpret_cast<uint4*>(Y + (size_t)(p0 + p) * Cout + co0 + c16) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-// Row-pair kernel for stride-1 convolutions with Wo <= 64 (instantiated for
-// 3x3 filters and Cin in {32, 64}).  A workgroup owns two output rows of one
-// image (64 columns, padded) and one 64-channel block of Cout.  It stages in
-// LDS once, with every global load of the staging in flight together:
-//   X  the R+1 input rows the two output rows touch, with the zero padding
+// Row-block kernel for stride-1 convolutions with Wo <= 64 (instantiated for
+// 3x3 filters and Cin in {32, 64}).  A workgroup owns ROWS output rows of one
+// image (64 columns, padded) and one block of WCO output channels, with
+// ROWS * WCO = 128 so that its 8 waves each own 32 pixels x 32 channels.  It
+// stages in LDS once, with every global load of the staging in flight
+// together:
+//   X  the ROWS+R-1 input rows the output rows touch, with the zero padding
 //      columns and rows materialised, [row][col][Cin bytes], 16-byte chunk
 //      c of column col at c ^ xswz(col) (conflict-free fragment reads);
-//   W  the 64 output channels' OHWI rows, pitch R*S*Cin + 16 bytes.
-// Each of the 8 waves then owns 32 output pixels x 32 channels and runs the
-// whole k = (r, s, ci) reduction from LDS (one v_mfma_i32_32x32x32_i8 per
-// 32-wide k-step, fully unrolled), so there is no im2col buffer and no
-// cross-wave reduction.  The requantized int8 results are stored straight from
-// registers, one dword (4 channels of a pixel) per store.
-constexpr int ROWS = 2;   // output rows per workgroup
-constexpr int PB = 64;    // output columns per row (padded)
-constexpr int RCOB = 64;  // output channels per workgroup
+//   W  the WCO output channels' OHWI rows, pitch R*S*Cin + 16 bytes.
+// Each wave then runs the whole k = (r, s, ci) reduction from LDS (one
+// v_mfma_i32_32x32x32_i8 per 32-wide k-step, fully unrolled), so there is no
+// im2col buffer and no cross-wave reduction.  The requantized int8 results
+// are stored straight from registers, one dword (4 channels of a pixel) per
+// store.
+constexpr int PB = 64;  // output columns per row (padded)
 
 template <int CIN>
 __device__ __forceinline__ int xswz(int col) {
   return (col * CIN / 256) & (CIN / 16 - 1);
 }
 
-template <int R, int S, int CIN>
+template <int R, int S, int CIN, int ROWS, int WCO>
 struct RowsGeom {
+  static_assert(ROWS * WCO == 128 && WCO % 32 == 0, "8 waves of 32 pixels x 32 channels");
+  static constexpr int NWC = WCO / 32;                      // 32-channel blocks per workgroup
   static constexpr int XR = ROWS + R - 1, XC = PB + S - 1;  // staged input rows / columns
   static constexpr int NCH = CIN / 16;                      // 16-byte chunks per pixel
   static constexpr int XTOT = XR * XC * NCH;                // X chunks
   static constexpr int RSC = R * S * CIN, WP = RSC + 16;    // weight row length / LDS pitch
-  static constexpr int WTOT = RCOB * RSC / 16;              // W chunks
+  static constexpr int WTOT = WCO * RSC / 16;               // W chunks
   static constexpr int XQ = (XTOT + 511) / 512, WQ = (WTOT + 511) / 512;
   static constexpr int X_BYTES = XR * XC * CIN;
-  static constexpr int LDS = X_BYTES + RCOB * WP;
+  static constexpr int LDS = X_BYTES + WCO * WP;
   static constexpr int T = R * S * CIN / 32;                // 32-wide k-steps
-  static_assert(LDS <= 65536, "row-pair conv LDS budget");
+  static_assert(LDS <= 65536, "row-block conv LDS budget");
 };
 
-template <int R, int S, int CIN>
+template <int R, int S, int CIN, int ROWS, int WCO>
 __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
                                                       const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
                                                       int H, int Wd, int Cout, int pad, int Ho, int Wo) {
-  using G = RowsGeom<R, S, CIN>;
+  using G = RowsGeom<R, S, CIN, ROWS, WCO>;
   __shared__ __attribute__((aligned(16))) int8_t smem[G::LDS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, fh = lane >> 5;
   const int rows_per_img = (Ho + ROWS - 1) / ROWS;
   const int n = blockIdx.x / rows_per_img;
   const int ho0 = (blockIdx.x % rows_per_img) * ROWS;
-  const int co0 = blockIdx.y * RCOB;
+  const int co0 = blockIdx.y * WCO;
   int8_t* const xs = smem;
   int8_t* const ws = smem + G::X_BYTES;
 
+  // wave: output row rr, pixels 32pb .. +32, channels 32wc .. +32
+  const int wc = wave % G::NWC, pb = (wave / G::NWC) & 1, rr = wave / (2 * G::NWC);
+
   // this lane's 16 output channels' shifts (4 per dword), loaded up front so
   // their latency hides under the staging
-  const int wc_ = wave & 1, fh_ = lane >> 5;
   uint32_t sh4[4];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) sh4[g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc_ + 8 * g + 4 * fh_);
+  for (int g = 0; g < 4; ++g) sh4[g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc + 8 * g + 4 * fh);
 
-  // ---- stage X (zero outside the image) and W: all loads first, then the LDS writes
+  // ---- stage X (zero outside the image) and W.  Every load is issued before
+  // any is waited for: positions outside the image load a valid dummy chunk
+  // and are zeroed by a select afterwards (a branch around the load would
+  // make the zero write wait for the load in flight to the same registers).
   v4i xv[G::XQ], wv[G::WQ];
+  bool xin[G::XQ];
 #pragma unroll
   for (int u = 0; u < G::XQ; ++u) {
     const int q = tid + 512 * u;
     const int c = q % G::NCH, rc = q / G::NCH;
     const int col = rc % G::XC, row = rc / G::XC;
     const int hi = ho0 + row - pad, wi = col - pad;
-    xv[u] = v4i{0};
-    if (q < G::XTOT && hi >= 0 && hi < H && wi >= 0 && wi < Wd)
-      xv[u] = *reinterpret_cast<const v4i*>(X + (((size_t)n * H + hi) * Wd + wi) * CIN + 16 * c);
+    xin[u] = q < G::XTOT && hi >= 0 && hi < H && wi >= 0 && wi < Wd;
+    const size_t off = xin[u] ? (((size_t)n * H + hi) * Wd + wi) * CIN + 16 * c : 0;
+    xv[u] = *reinterpret_cast<const v4i*>(X + off);
   }
 #pragma unroll
   for (int u = 0; u < G::WQ; ++u) {
     const int q = tid + 512 * u;
-    if (q < G::WTOT)
-      wv[u] = *reinterpret_cast<const v4i*>(W + (size_t)co0 * G::RSC + 16 * (size_t)q);
+    wv[u] = *reinterpret_cast<const v4i*>(W + (size_t)co0 * G::RSC + 16 * (size_t)(q < G::WTOT ? q : 0));
   }
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
+
+  // The accumulators start at the rounding term 2^(s-1) of their channel
+  // (|acc| <= R*S*CIN * 2^14 < 2^30 keeps acc + 2^30 inside int32), so the
+  // epilogue only shifts and saturates.  Computed here, while the staging
+  // loads are in flight (the shifts were issued first).
+  v16i acc;
+  int smin = 31;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int sc = (sh4[g] >> (8 * tt)) & 31;
+      acc[4 * g + tt] = (int)((1u << sc) >> 1);
+      smin = min(smin, sc);
+    }
+  const bool hi_form = __builtin_amdgcn_ballot_w64(smin < 8) == 0;  // every shift of the wave >= 8
+  __builtin_amdgcn_sched_barrier(0);
+
 #pragma unroll
   for (int u = 0; u < G::XQ; ++u) {
     const int q = tid + 512 * u;
     const int c = q % G::NCH, rc = q / G::NCH;
     const int col = rc % G::XC, row = rc / G::XC;
-    if (q < G::XTOT) *reinterpret_cast<v4i*>(xs + (row * G::XC + col) * CIN + ((c ^ xswz<CIN>(col)) << 4)) = xv[u];
+    if (q < G::XTOT)
+      *reinterpret_cast<v4i*>(xs + (row * G::XC + col) * CIN + ((c ^ xswz<CIN>(col)) << 4)) = xin[u] ? xv[u] : v4i{0};
   }
 #pragma unroll
   for (int u = 0; u < G::WQ; ++u) {
@@ -237,11 +264,8 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   }
   __syncthreads();
 
-  // ---- wave: output row rr, pixels 32pb .. +32, channels 32wc .. +32
-  const int rr = wave >> 2, pb = (wave >> 1) & 1, wc = wave & 1;
   const int px = 32 * pb + fr;
   const int8_t* wrow = ws + (32 * wc + fr) * G::WP + 16 * fh;
-  v16i acc = v16i{0};
 #pragma unroll
   for (int t = 0; t < G::T; ++t) {
     const int cib = t % (CIN / 32), rs = t / (CIN / 32);
@@ -260,19 +284,30 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   const int ho = ho0 + rr;
   if (ho < Ho && px < Wo) {
     int8_t* const y = Y + (((size_t)n * Ho + ho) * Wo + px) * Cout + co0 + 32 * wc + 4 * fh;
+    if (hi_form) {
+      // s >= 8: y is the high byte of sat_int16(acc >> (s - 8)) (floor
+      // shifts compose; saturating at 16 bits clamps the high byte exactly
+      // at -128 and 127), 7 instructions per 4 channels
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        // round half up, shift, saturate: |acc| <= 576 * 2^14, so adding
-        // 2^(s-1) cannot overflow for any s <= 31
-        const int sc = (sh4[g] >> (8 * tt)) & 0xFF;
-        const int rnd = (1 << sc) >> 1;
-        const int q = min(max((acc[4 * g + tt] + rnd) >> sc, -128), 127);
-        packed |= (uint32_t)(q & 0xFF) << (8 * tt);
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t sm8 = sh4[g] - 0x08080808u;  // bytewise s - 8 (no borrow: every byte >= 8)
+        const int u0 = acc[4 * g] >> (sm8 & 31), u1 = acc[4 * g + 1] >> ((sm8 >> 8) & 31);
+        const int u2 = acc[4 * g + 2] >> ((sm8 >> 16) & 31), u3 = acc[4 * g + 3] >> ((sm8 >> 24) & 31);
+        const uint32_t p01 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(u0, u1));
+        const uint32_t p23 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(u2, u3));
+        *reinterpret_cast<uint32_t*>(y + 8 * g) = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
       }
-      *reinterpret_cast<uint32_t*>(y + 8 * g) = packed;
+    } else {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const int q = min(max(acc[4 * g + tt] >> ((sh4[g] >> (8 * tt)) & 31), -128), 127);
+          packed |= (uint32_t)(q & 0xFF) << (8 * tt);
+        }
+        *reinterpret_cast<uint32_t*>(y + 8 * g) = packed;
+      }
     }
   }
 }
@@ -306,28 +341,43 @@ __global__ __launch_bounds__(256) void conv2d_i8_direct(const int8_t* __restrict
   Y[idx] = (int8_t)requant1((int)acc, shifts[co]);
 }
 
+template <int CIN, int ROWS, int WCO>
+void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
+                    int H, int Wd, int Cout, int pad, int Ho, int Wo) {
+  dim3 grid((unsigned)(N * ((Ho + ROWS - 1) / ROWS)), Cout / WCO);
+  hipLaunchKernelGGL((conv2d_i8_rows<3, 3, CIN, ROWS, WCO>), grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd, Cout,
+                     pad, Ho, Wo);
+}
+
 }  // namespace
 
 namespace miaie {
+
+// Row-block shape: 4 output rows x 32 channels stages fewer bytes per
+// workgroup (X 6 rows + W 32 rows) than 2 rows x 64 channels (X 4 rows + W 64
+// rows) when Cout is not a multiple of 64 or the weights dominate.
+template <int CIN>
+static int launch_rows(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
+                       int H, int Wd, int Cout, int pad, int Ho, int Wo) {
+  if (Cout % 64 == 0)
+    launch_rows_as<CIN, 2, 64>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
+  else
+    launch_rows_as<CIN, 4, 32>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
+  return check_launch(ctx, "conv2d_i8_rows");
+}
 
 int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y,
                      int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad) {
   const int Ho = (H + 2 * pad - R) / stride + 1;
   const int Wo = (Wd + 2 * pad - S) / stride + 1;
   const size_t P = (size_t)N * Ho * Wo;
-  // Row-pair kernel (3x3, stride 1, Cin 32 or 64, Wo <= 64).
-  const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64) && Cout % RCOB == 0 &&
+  // Row-block kernel (3x3, stride 1, Cin 32 or 64, Wo <= 64).
+  const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64) && Cout % 32 == 0 &&
                        Wo <= PB && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) && aligned(shifts, 4) &&
-                       (size_t)N * ((Ho + ROWS - 1) / ROWS) < ((size_t)1 << 31);
+                       (size_t)N * Ho < ((size_t)1 << 31);
   if (rows_ok) {
-    dim3 grid((unsigned)(N * ((Ho + ROWS - 1) / ROWS)), Cout / RCOB);
-    if (Cin == 64)
-      hipLaunchKernelGGL((conv2d_i8_rows<3, 3, 64>), grid, dim3(512), 0, ctx->stream, X, W, shifts, Y, H, Wd, Cout,
-                         pad, Ho, Wo);
-    else
-      hipLaunchKernelGGL((conv2d_i8_rows<3, 3, 32>), grid, dim3(512), 0, ctx->stream, X, W, shifts, Y, H, Wd, Cout,
-                         pad, Ho, Wo);
-    return check_launch(ctx, "conv2d_i8_rows");
+    if (Cin == 64) return launch_rows<64>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
+    return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
   }
   const bool fast = Cin % 32 == 0 && Cout % COB == 0 && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) &&
                     P < ((size_t)1 << 31) && (P + PIX - 1) / PIX < ((size_t)1 << 31);

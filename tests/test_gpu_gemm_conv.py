@@ -204,6 +204,8 @@ CONV_SHAPES = [
     (2, 6, 50, 64, 128, 3, 3, 1, 0),  # row-pair, no padding, two Cout blocks
     (1, 9, 60, 64, 64, 3, 3, 1, 2),   # row-pair, pad 2 (two zero columns each side)
     (1, 4, 64, 64, 64, 3, 3, 1, 0),   # row-pair, widest row, no padding
+    (1, 7, 56, 64, 32, 3, 3, 1, 1),   # row-block 4 rows x 32 channels (Cout 32), last block half outside
+    (2, 5, 30, 32, 96, 3, 3, 1, 1),   # row-block 4 x 32, three channel blocks, Cin 32
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # fallback kernel (channels not multiples of 32/64)
     (2, 6, 7, 3, 5, 3, 3, 2, 0),      # fallback kernel
 ]
@@ -225,6 +227,42 @@ def test_conv2d_i8(ctx, shape):
     ctx.wait(60_000)
     Yg = ctx.download(dY)
     assert np.array_equal(Yg, oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad))
+
+
+@pytest.mark.parametrize("shape", [
+    (1, 6, 56, 64, 64, 3, 3, 1, 1),   # row-block 2 rows x 64 channels
+    (1, 5, 20, 32, 96, 3, 3, 1, 1),   # row-block 4 rows x 32 channels
+    (1, 8, 8, 64, 64, 3, 3, 2, 1),    # implicit-GEMM kernel
+    (1, 5, 5, 4, 8, 3, 3, 1, 1),      # direct kernel
+])
+@pytest.mark.parametrize("small", [False, True])
+def test_conv2d_i8_shift_range(ctx, shape, small):
+    """Per-channel shifts over the whole documented range [0, 31], mixed
+    within each 32-channel block (so waves take the general epilogue), then
+    with every shift >= 8 but one channel at 7, and with every shift >= 8
+    (the high-byte epilogue).  `small` draws X in [-3, 3] so that small
+    shifts land inside the int8 range instead of saturating."""
+    N, H, W, Cin, Cout, R, S, stride, pad = shape
+    _say("conv2d shift range", shape, small)
+    rng = np.random.default_rng(7 + Cout + small)
+    lo, hi = (-3, 4) if small else (-128, 128)
+    X = rng.integers(lo, hi, size=(N, H, W, Cin), dtype=np.int8)
+    Wt = rng.integers(-128, 128, size=(Cout, R, S, Cin), dtype=np.int8)
+    Ho = (H + 2 * pad - R) // stride + 1
+    Wo = (W + 2 * pad - S) // stride + 1
+    full = rng.integers(0, 32, size=Cout, dtype=np.uint8)
+    full[:4] = [0, 31, 7, 8]
+    one7 = rng.integers(8, 32, size=Cout, dtype=np.uint8)
+    one7[Cout // 2 + 1] = 7
+    ge8 = rng.integers(8, 32, size=Cout, dtype=np.uint8)
+    ge8[:2] = [8, 31]
+    dX, dW = ctx.upload(X), ctx.upload(Wt)
+    for sh in (full, one7, ge8):
+        dS = ctx.upload(sh)
+        dY = ctx.empty((N, Ho, Wo, Cout), np.int8)
+        ctx.conv2d_i8_nhwc(dX, dW, dS, dY, N, H, W, Cin, Cout, R, S, stride, pad)
+        ctx.wait(60_000)
+        assert np.array_equal(ctx.download(dY), oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad)), sh
 
 
 def test_conv2d_i8_config(ctx):
