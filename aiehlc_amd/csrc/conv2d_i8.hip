@@ -174,10 +174,18 @@ struct RowsGeom {
   static constexpr int NWC = WCO / 32;                      // 32-channel blocks per workgroup
   static constexpr int XR = ROWS + R - 1, XC = PB + S - 1;  // staged input rows / columns
   static constexpr int NCH = CIN / 16;                      // 16-byte chunks per pixel
-  static constexpr int XTOT = XR * XC * NCH;                // X chunks
+  // X staging map: one pass covers RPP whole rows of the first PB staged
+  // columns (thread -> chunk tid % NCH of column tid / NCH % PB), XQ passes
+  // cover the XR rows, and one more load per thread (the first XE threads)
+  // covers the last S - 1 columns of every row.
+  static constexpr int RPP = 512 / (PB * NCH);              // rows per pass
+  static constexpr int XQ = (XR + RPP - 1) / RPP;           // passes
+  static constexpr int XE = XR * (XC - PB) * NCH;           // chunks of the last S - 1 columns
   static constexpr int RSC = R * S * CIN, WP = RSC + 16;    // weight row length / LDS pitch
   static constexpr int WTOT = WCO * RSC / 16;               // W chunks
-  static constexpr int XQ = (XTOT + 511) / 512, WQ = (WTOT + 511) / 512;
+  static constexpr int WQ = (WTOT + 511) / 512;
+  static constexpr int WREM = WTOT - 512 * (WQ - 1);        // W chunks of the last pass
+  static_assert(512 % (PB * NCH) == 0 && XE <= 512, "row-block conv staging map");
   static constexpr int X_BYTES = XR * XC * CIN;
   static constexpr int LDS = X_BYTES + WCO * WP;
   static constexpr int T = R * S * CIN / 32;                // 32-wide k-steps
@@ -192,9 +200,8 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   __shared__ __attribute__((aligned(16))) int8_t smem[G::LDS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, fh = lane >> 5;
-  const int rows_per_img = (Ho + ROWS - 1) / ROWS;
-  const int n = blockIdx.x / rows_per_img;
-  const int ho0 = (blockIdx.x % rows_per_img) * ROWS;
+  const int n = blockIdx.z;
+  const int ho0 = blockIdx.x * ROWS;
   const int co0 = blockIdx.y * WCO;
   int8_t* const xs = smem;
   int8_t* const ws = smem + G::X_BYTES;
@@ -209,26 +216,34 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   for (int g = 0; g < 4; ++g) sh4[g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc + 8 * g + 4 * fh);
 
   // ---- stage X (zero outside the image) and W.  Every load is issued before
-  // any is waited for: positions outside the image load a valid dummy chunk
-  // and are zeroed by a select afterwards (a branch around the load would
+  // any is waited for: positions outside the image load the nearest chunk
+  // inside it and are zeroed by a select afterwards (a branch around the load would
   // make the zero write wait for the load in flight to the same registers).
-  v4i xv[G::XQ], wv[G::WQ];
-  bool xin[G::XQ];
-#pragma unroll
-  for (int u = 0; u < G::XQ; ++u) {
-    const int q = tid + 512 * u;
-    const int c = q % G::NCH, rc = q / G::NCH;
-    const int col = rc % G::XC, row = rc / G::XC;
+  // Offsets are 32-bit from the tensor base (the launcher checks the sizes).
+  const int xc = tid % G::NCH, xcol = (tid / G::NCH) % PB, xrow = tid / (G::NCH * PB);
+  // (threads past XE repeat an earlier thread's chunk: the same value to the
+  // same LDS address, so the load and the write need no branch)
+  const int et = tid % G::XE;
+  const int ec = et % G::NCH, ecol = PB + (et / G::NCH) % (G::XC - PB), erow = et / (G::NCH * (G::XC - PB));
+  auto x_off = [&](int row, int col, int c, bool& in) -> uint32_t {
     const int hi = ho0 + row - pad, wi = col - pad;
-    xin[u] = q < G::XTOT && hi >= 0 && hi < H && wi >= 0 && wi < Wd;
-    const size_t off = xin[u] ? (((size_t)n * H + hi) * Wd + wi) * CIN + 16 * c : 0;
-    xv[u] = *reinterpret_cast<const v4i*>(X + off);
-  }
+    in = (unsigned)hi < (unsigned)H && (unsigned)wi < (unsigned)Wd;
+    // clamped into the image: a valid address without a branch
+    const int hc = min(max(hi, 0), H - 1), wcl = min(max(wi, 0), Wd - 1);
+    return (uint32_t)(((n * H + hc) * Wd + wcl) * CIN + 16 * c);
+  };
+  v4i xv[G::XQ], xe, wv[G::WQ];
+  bool xin[G::XQ], ein;
+  // (a pass that runs past the last staged row repeats that row's chunks)
+  auto xrow_of = [&](int u) { return min(G::RPP * u + xrow, G::XR - 1); };
 #pragma unroll
-  for (int u = 0; u < G::WQ; ++u) {
-    const int q = tid + 512 * u;
-    wv[u] = *reinterpret_cast<const v4i*>(W + (size_t)co0 * G::RSC + 16 * (size_t)(q < G::WTOT ? q : 0));
-  }
+  for (int u = 0; u < G::XQ; ++u)
+    xv[u] = *reinterpret_cast<const v4i*>(X + x_off(xrow_of(u), xcol, xc, xin[u]));
+  xe = *reinterpret_cast<const v4i*>(X + x_off(erow, ecol, ec, ein));
+  // (threads past the end of the last W pass repeat that pass's chunks)
+  auto wq_of = [&](int u) { return u < G::WQ - 1 ? tid + 512 * u : 512 * (G::WQ - 1) + tid % G::WREM; };
+#pragma unroll
+  for (int u = 0; u < G::WQ; ++u) wv[u] = *reinterpret_cast<const v4i*>(W + (uint32_t)(co0 * G::RSC + 16 * wq_of(u)));
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
 
   // The accumulators start at the rounding term 2^(s-1) of their channel
@@ -248,19 +263,16 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   const bool hi_form = __builtin_amdgcn_ballot_w64(smin < 8) == 0;  // every shift of the wave >= 8
   __builtin_amdgcn_sched_barrier(0);
 
+  auto x_put = [&](int row, int col, int c, bool in, v4i v) {
+    *reinterpret_cast<v4i*>(xs + (row * G::XC + col) * CIN + ((c ^ xswz<CIN>(col)) << 4)) = in ? v : v4i{0};
+  };
 #pragma unroll
-  for (int u = 0; u < G::XQ; ++u) {
-    const int q = tid + 512 * u;
-    const int c = q % G::NCH, rc = q / G::NCH;
-    const int col = rc % G::XC, row = rc / G::XC;
-    if (q < G::XTOT)
-      *reinterpret_cast<v4i*>(xs + (row * G::XC + col) * CIN + ((c ^ xswz<CIN>(col)) << 4)) = xin[u] ? xv[u] : v4i{0};
-  }
+  for (int u = 0; u < G::XQ; ++u) x_put(xrow_of(u), xcol, xc, xin[u], xv[u]);
+  x_put(erow, ecol, ec, ein, xe);
 #pragma unroll
   for (int u = 0; u < G::WQ; ++u) {
-    const int q = tid + 512 * u;
-    const int c = q % (G::RSC / 16), row = q / (G::RSC / 16);
-    if (q < G::WTOT) *reinterpret_cast<v4i*>(ws + row * G::WP + 16 * c) = wv[u];
+    const int q = wq_of(u);
+    *reinterpret_cast<v4i*>(ws + (q / (G::RSC / 16)) * G::WP + 16 * (q % (G::RSC / 16))) = wv[u];
   }
   __syncthreads();
 
@@ -283,7 +295,7 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   // barrier).
   const int ho = ho0 + rr;
   if (ho < Ho && px < Wo) {
-    int8_t* const y = Y + (((size_t)n * Ho + ho) * Wo + px) * Cout + co0 + 32 * wc + 4 * fh;
+    int8_t* const y = Y + (uint32_t)(((n * Ho + ho) * Wo + px) * Cout + co0 + 32 * wc + 4 * fh);
     if (hi_form) {
       // s >= 8: y is the high byte of sat_int16(acc >> (s - 8)) (floor
       // shifts compose; saturating at 16 bits clamps the high byte exactly
@@ -344,7 +356,7 @@ __global__ __launch_bounds__(256) void conv2d_i8_direct(const int8_t* __restrict
 template <int CIN, int ROWS, int WCO>
 void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
                     int H, int Wd, int Cout, int pad, int Ho, int Wo) {
-  dim3 grid((unsigned)(N * ((Ho + ROWS - 1) / ROWS)), Cout / WCO);
+  dim3 grid((unsigned)((Ho + ROWS - 1) / ROWS), Cout / WCO, N);
   hipLaunchKernelGGL((conv2d_i8_rows<3, 3, CIN, ROWS, WCO>), grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd, Cout,
                      pad, Ho, Wo);
 }
@@ -374,7 +386,8 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
   // Row-block kernel (3x3, stride 1, Cin 32 or 64, Wo <= 64).
   const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64) && Cout % 32 == 0 &&
                        Wo <= PB && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) && aligned(shifts, 4) &&
-                       (size_t)N * Ho < ((size_t)1 << 31);
+                       N <= 65535 && (size_t)N * H * Wd * Cin < ((size_t)1 << 31) &&
+                       (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31);
   if (rows_ok) {
     if (Cin == 64) return launch_rows<64>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
     return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
