@@ -407,11 +407,13 @@ def main() -> int:
         roof = min(PEAK_INT8_TOPS, conv_ops / conv_bytes * PEAK_HBM_GBS / 1e3)
         extras["conv2d_3x3"] = {
             "config": "N=8 H=W=56 Cin=Cout=64 3x3 stride 1 pad 1, NHWC x OHWI, per-channel shift in [8,12]",
-            "kernel": "conv2d_i8_rows<3,3,64>",
+            "kernel": "conv2d_i8_rows<3,3,64,2,64> (2 output rows x 64 channels per workgroup)",
             "us_per_step": round(ms_c * 1e3, 3),
             "gops": round(conv_ops / (ms_c * 1e-3) / 1e9, 1),
             "alg_GBps": round(conv_bytes / (ms_c * 1e-3) / 1e9, 1),
-            "roofline": {"bound": "hbm", "alg_bytes": conv_bytes, "roof_tops": round(roof, 1),
+            "roofline": {"bound": "hbm", "achieved": round(conv_bytes / (ms_c * 1e-3) / 1e9, 1),
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "alg_bytes": conv_bytes,
+                         "roof_tops": round(roof, 1),
                          "frac": round(conv_ops / (ms_c * 1e-3) / 1e12 / roof, 4)},
             "graph_chain": {"convs_per_replay": chain, "us_per_conv": round(ms_cg * 1e3, 3),
                             "gops": round(conv_ops / (ms_cg * 1e-3) / 1e9, 1),
