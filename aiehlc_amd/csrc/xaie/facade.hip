@@ -9,6 +9,7 @@
 #include <sys/mman.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdarg>
 #include <cstdio>
@@ -40,35 +41,83 @@ struct TileList {
   u32 off[kMaxRunTiles];
 };
 
+// A single-tile launch of a built-in carries the tile's queued host -> tile
+// copies and a request to mirror its output window into pinned host memory,
+// so that the flow "move in, run, wait, move out" is one launch: the copies
+// run in the kernel's prologue (reading the pinned staging buffer over PCIe),
+// the output window is copied to the host shadow in its epilogue, and `seq`
+// is published in a host flag once both are there.
+constexpr int kFuseCopies = 4;
+struct FuseArgs {
+  u32 ncopy;
+  u32 dst[kFuseCopies];              // tile-relative byte offsets
+  u32 size[kFuseCopies];
+  const uint8_t* src[kFuseCopies];   // pinned staging
+  uint8_t* shadow;                   // pinned host mirror of the output window, or null
+  u32 shadow_addr, shadow_size;
+  uint32_t* flag;                    // host word that receives seq, or null
+  uint32_t seq;
+};
+
+__device__ void block_copy(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, u32 n) {
+  if ((((uintptr_t)dst | (uintptr_t)src) & 15) == 0) {
+    for (u32 i = threadIdx.x; i < n / 16; i += blockDim.x)
+      reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+    for (u32 i = n / 16 * 16 + threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+  } else {
+    for (u32 i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
+__device__ void fuse_in(uint8_t* base, const FuseArgs& f) {
+  for (u32 c = 0; c < f.ncopy; ++c) block_copy(base + f.dst[c], f.src[c], f.size[c]);
+  __syncthreads();
+}
+
+__device__ void fuse_out(uint8_t* base, const FuseArgs& f) {
+  __syncthreads();
+  if (f.shadow) block_copy(f.shadow, base + f.shadow_addr, f.shadow_size);
+  if (f.flag) {
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(f.flag, f.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 // `mm` (aieml_mm.cc:41-93) and `perf` (aieml_perf.cc:61-83): the input
 // window holds A[n][n] then B as [n][k] (n*n words each); out[i][j] =
 // sum_k A[i][k] * B[j][k] in 32-bit wrap-around arithmetic.  n <= 16, so one
 // workgroup of 256 lanes covers a tile's whole output.
 __global__ __launch_bounds__(256) void tile_mm_nt(uint8_t* __restrict__ mem, TileList tl, u32 in_addr, u32 out_addr,
-                                                  int n, u32 passes) {
+                                                  int n, u32 passes, FuseArgs fz) {
   uint8_t* base = mem + tl.off[blockIdx.x];
+  fuse_in(base, fz);
   const uint32_t* a = reinterpret_cast<const uint32_t*>(base + in_addr);
   const uint32_t* bt = a + n * n;
   uint32_t* out = reinterpret_cast<uint32_t*>(base + out_addr);
   const int t = threadIdx.x;
-  if (t >= n * n) return;
-  const int i = t / n, j = t - i * n;
-  for (u32 p = 0; p < passes; ++p) {
-    uint32_t acc = 0;
-    for (int k = 0; k < n; ++k) acc += a[i * n + k] * bt[j * n + k];
-    out[t] = acc;
+  if (t < n * n) {
+    const int i = t / n, j = t - i * n;
+    for (u32 p = 0; p < passes; ++p) {
+      uint32_t acc = 0;
+      for (int k = 0; k < n; ++k) acc += a[i * n + k] * bt[j * n + k];
+      out[t] = acc;
+    }
   }
+  fuse_out(base, fz);
 }
 
 // `k1` / `k2` (multi_tile.cpp:39-47, seq_full_col.cpp:39-47): 20 words of
 // out = in[0] + addend.
 __global__ __launch_bounds__(64) void tile_add20(uint8_t* __restrict__ mem, TileList tl, u32 in_addr, u32 out_addr,
-                                                 int addend, u32 passes) {
+                                                 int addend, u32 passes, FuseArgs fz) {
   uint8_t* base = mem + tl.off[blockIdx.x];
+  fuse_in(base, fz);
   const int32_t* in = reinterpret_cast<const int32_t*>(base + in_addr);
   int32_t* out = reinterpret_cast<int32_t*>(base + out_addr);
-  if (threadIdx.x >= 20) return;
-  for (u32 p = 0; p < passes; ++p) out[threadIdx.x] = (int32_t)((uint32_t)in[0] + (uint32_t)addend);
+  if (threadIdx.x < 20)
+    for (u32 p = 0; p < passes; ++p) out[threadIdx.x] = (int32_t)((uint32_t)in[0] + (uint32_t)addend);
+  fuse_out(base, fz);
 }
 
 // `mm` of vek385_verification.cpp:56-69: out = in . in over 3x3 uint64, the
@@ -93,12 +142,40 @@ __global__ __launch_bounds__(64) void tile_mm3_u64(uint8_t* __restrict__ mem, Ti
   }
 }
 
+// Host <-> tile copy through the pinned staging buffer, which this kernel
+// reads or writes over PCIe directly: small moves skip the DMA engine, whose
+// per-copy start-up latency is most of their cost.  16-byte words when both
+// ends are 16-byte aligned, bytes otherwise.  With `flag` (host memory), one
+// workgroup copies everything and then publishes `seq` there, after a
+// system-scope fence, so the host can read the bytes as soon as they have
+// landed instead of waiting for the kernel's completion signal.
+__global__ __launch_bounds__(256) void stage_copy(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                  size_t n, uint32_t* flag, uint32_t seq) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if ((((uintptr_t)dst | (uintptr_t)src) & 15) == 0) {
+    const size_t nv = n / 16;
+    for (size_t i = t0; i < nv; i += stride)
+      reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+    for (size_t i = nv * 16 + t0; i < n; i += stride) dst[i] = src[i];
+  } else {
+    for (size_t i = t0; i < n; i += stride) dst[i] = src[i];
+  }
+  if (flag) {
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- built-in descriptors
 extern "C" {
 MIAIE_XAIE_API const XAie_MiaieKernel miaie_xaie_mm = {
     MIAIE_XAIE_KERNEL_MAGIC, "mm", 2, {0x1000, 0x6000}, {512, 512}, 0, nullptr, nullptr, B_MM_NT};
+MIAIE_XAIE_API const XAie_MiaieKernel miaie_xaie_mm8 = {
+    MIAIE_XAIE_KERNEL_MAGIC, "mm", 2, {0x1000, 0x6000}, {128, 128}, 0, nullptr, nullptr, B_MM_NT};
 MIAIE_XAIE_API const XAie_MiaieKernel miaie_xaie_perf = {
     MIAIE_XAIE_KERNEL_MAGIC, "perf", 2, {0x1000, 0x6000}, {512, 512}, 0, nullptr, nullptr, B_MM_NT};
 MIAIE_XAIE_API const XAie_MiaieKernel miaie_xaie_k1 = {
@@ -150,6 +227,22 @@ struct Core {
   bool pending = false;    // enabled, launch not issued yet
   bool ran = false;
   uint64_t seq = 0;        // launch batch of the last run
+  bool fused = false;      // the last run was a fused single-tile launch ...
+  uint32_t fused_seq = 0;  // ... that publishes this number in the host done flag
+};
+
+struct PendCopy {          // a staged host -> tile copy not yet issued
+  int tile;
+  uint64_t addr;
+  const uint8_t* src;      // slice of the pinned staging buffer
+  size_t size;
+};
+
+struct Shadow {            // pinned host mirror of a tile's output window
+  bool valid = false;
+  uint64_t addr = 0;
+  u32 size = 0;
+  uint32_t seq = 0;        // fused launch that writes it
 };
 
 struct Route {
@@ -185,7 +278,14 @@ struct miaie_xaie_dev {
   std::deque<std::pair<uint64_t, hipEvent_t>> inflight;  // launch batches not yet seen complete
   std::vector<hipEvent_t> spare;
   uint64_t issued = 0, completed = 0;
-  uint8_t* stage = nullptr;        // pinned host staging for host <-> tile copies
+  uint8_t* stage = nullptr;        // pinned, coherent host staging for host <-> tile copies
+  uint32_t* stage_flag = nullptr;  // after it: tile -> host copies publish their sequence number here
+  uint32_t stage_seq = 0;
+  uint32_t* done_flag = nullptr;   // fused launches publish their sequence number here
+  uint32_t fuse_seq = 0;
+  uint8_t* shadow_mem = nullptr;   // after the flags: kShadowSlot bytes per tile
+  std::vector<PendCopy> pend;      // host -> tile copies waiting for the next launch
+  std::vector<Shadow> shadow;      // per tile
   size_t stage_used = 0;           // bytes of it taken since the stream last drained
   hipEvent_t stage_ev = nullptr;   // recorded after the latest staged host -> tile copy
   XAie_BackendType backend = XAIE_IO_BACKEND_BAREMETAL;
@@ -286,6 +386,15 @@ AieRC record_batch(miaie_xaie_dev* d, uint64_t* seq) {
 }
 
 // Window addresses of a kernel (the reference compiler's placement rule).
+// n of an mm-type kernel: its input window holds A and B, 2 n^2 words, so a
+// size_hint of 2 n^2 (n <= 16) fixes n; otherwise the examples' 16.
+u32 window_n(const XAie_MiaieKernel* k) {
+  if (k->Builtin == B_MM_NT)
+    for (u32 n = 1; n <= 16; ++n)
+      if (k->SizeHint[0] == 2 * n * n) return n;
+  return 16;
+}
+
 void window_layout(const XAie_MiaieKernel* k, u32* ping, u32* pong) {
   u32 addr = 0x1000;
   for (u32 i = 0; i < k->NumParams; ++i) {
@@ -328,10 +437,221 @@ AieRC check_windows(miaie_xaie_dev* d, const XAie_MiaieKernel* k, u32 arg, u32 t
   return XAIE_OK;
 }
 
+// Host <-> tile copies up to kStageBytes go through a pinned, coherent
+// staging buffer that the GPU reads and writes directly.
+//   host -> tile: the source bytes are copied into a slice of the buffer and
+//     the copy is queued.  The next single-tile launch of a built-in on that
+//     tile carries it in its prologue (one launch for "move in, run"); any
+//     other operation first issues the queued copies as copy kernels.  Either
+//     way the device copy runs in stream order ahead of later work, as an AIE
+//     DMA runs on after XAie_MoveData returns (the perf example waits for it
+//     with XAie_RouteDmaWait, aieml_perf.cc:156-163).
+//   tile -> host: returns once the bytes are in the destination.  A range
+//     inside the output window of the tile's last fused launch is read from
+//     that launch's host shadow once its done flag is up; otherwise a copy
+//     kernel writes the staging buffer and publishes a flag.
+// Larger copies take the synchronous miaie copies.  Staged slices are taken
+// consecutively; when the buffer is full, the stream is drained and it starts
+// over.
+constexpr size_t kStageBytes = 4u << 20;
+constexpr size_t kShadowSlot = 4u << 10;  // largest output window mirrored per tile
+
+AieRC ensure_stage(miaie_xaie_dev* d) {
+  hipError_t e = hipSetDevice(d->device);
+  if (e != hipSuccess) return hip_fail(d, e, "hipSetDevice");
+  if (!d->stage) {
+    const size_t bytes = kStageBytes + 256 + kShadowSlot * d->cores.size();
+    e = hipHostMalloc(reinterpret_cast<void**>(&d->stage), bytes, hipHostMallocCoherent);
+    if (e != hipSuccess) {
+      d->stage = nullptr;
+      return hip_fail(d, e, "pinned staging buffer");
+    }
+    d->stage_flag = reinterpret_cast<uint32_t*>(d->stage + kStageBytes);
+    d->done_flag = d->stage_flag + 1;
+    d->shadow_mem = d->stage + kStageBytes + 256;
+    __atomic_store_n(d->stage_flag, d->stage_seq = 0, __ATOMIC_RELEASE);
+    __atomic_store_n(d->done_flag, d->fuse_seq = 0, __ATOMIC_RELEASE);
+    d->stage_used = 0;
+  }
+  if (!d->stage_ev) {
+    e = hipEventCreateWithFlags(&d->stage_ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      d->stage_ev = nullptr;
+      return hip_fail(d, e, "hipEventCreate");
+    }
+  }
+  return XAIE_OK;
+}
+
+unsigned stage_blocks(size_t size) { return (unsigned)std::min<size_t>((size + 4095) / 4096, 1024); }
+
+// Issue the queued host -> tile copies as copy kernels.
+AieRC issue_pending(miaie_xaie_dev* d) {
+  if (d->pend.empty()) return XAIE_OK;
+  hipError_t e = hipSuccess;
+  for (const PendCopy& c : d->pend) {
+    stage_copy<<<stage_blocks(c.size), 256, 0, d->stream>>>(d->mem + d->off[c.tile] + c.addr, c.src, c.size, nullptr,
+                                                            0);
+    e = hipGetLastError();
+    if (e != hipSuccess) break;
+  }
+  d->pend.clear();
+  if (e == hipSuccess) e = hipEventRecord(d->stage_ev, d->stream);
+  return e == hipSuccess ? XAIE_OK : hip_fail(d, e, "host to tile copy");
+}
+
+AieRC stage_take(miaie_xaie_dev* d, size_t size, uint8_t** slice) {
+  if (AieRC rc = ensure_stage(d)) return rc;
+  const size_t need = (size + 255) & ~static_cast<size_t>(255);
+  if (d->stage_used + need > kStageBytes) {
+    if (AieRC rc = issue_pending(d)) return rc;
+    hipError_t e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) return hip_fail(d, e, "waiting for staged copies");
+    d->stage_used = 0;
+  }
+  *slice = d->stage + d->stage_used;
+  d->stage_used += need;
+  return XAIE_OK;
+}
+
+// Anything that writes a tile's memory outside a fused launch makes its
+// shadow stale.
+void invalidate_shadow(miaie_xaie_dev* d, int t) {
+  if (t >= 0 && (size_t)t < d->shadow.size()) d->shadow[t].valid = false;
+}
+
+AieRC copy_h2d(miaie_xaie_dev* d, int t, uint64_t addr, const void* src, size_t size) {
+  if (size == 0) return XAIE_OK;
+  invalidate_shadow(d, t);
+  if (size <= kStageBytes) {
+    if (d->pend.size() >= (size_t)kFuseCopies)
+      if (AieRC rc = issue_pending(d)) return rc;
+    uint8_t* st = nullptr;
+    if (AieRC rc = stage_take(d, size, &st)) return rc;
+    std::memcpy(st, src, size);
+    d->pend.push_back(PendCopy{t, addr, st, size});
+    return XAIE_OK;
+  }
+  if (AieRC rc = issue_pending(d)) return rc;
+  const int rc = miaie_copy_h2d(d->ctx, d->mem + d->off[t] + addr, src, size);
+  return rc ? miaie_fail(d, rc, "host to tile copy") : XAIE_OK;
+}
+
+// Spin until the host word `flag` reaches `seq` (wrap-safe), for up to
+// kFlagSpinUs; false if it did not.
+constexpr int kFlagSpinUs = 2000;
+bool spin_flag(const uint32_t* flag, uint32_t seq) {
+  const auto deadline = std::chrono::steady_clock::now() + std::chrono::microseconds(kFlagSpinUs);
+  for (;;) {
+    if ((int32_t)(__atomic_load_n(flag, __ATOMIC_ACQUIRE) - seq) >= 0) return true;
+    if (std::chrono::steady_clock::now() >= deadline) return false;
+  }
+}
+
+// Tile -> host copies up to kFlagCopyBytes run in one workgroup that
+// publishes a sequence number in the staging buffer's flag word once the
+// bytes are there; the host spins on it and then falls back to waiting for
+// the stream (which also reports a failed launch).
+constexpr size_t kFlagCopyBytes = 64u << 10;
+
+AieRC copy_d2h(miaie_xaie_dev* d, int t, uint64_t addr, void* dst, size_t size) {
+  if (size == 0) return XAIE_OK;
+  const Shadow& sh = d->shadow[t];
+  if (sh.valid && addr >= sh.addr && addr + size <= sh.addr + sh.size) {
+    if (!spin_flag(d->done_flag, sh.seq)) {
+      if (AieRC rc = issue_pending(d)) return rc;
+      hipError_t e = hipStreamSynchronize(d->stream);
+      if (e != hipSuccess) return hip_fail(d, e, "tile to host copy");
+    }
+    std::memcpy(dst, d->shadow_mem + (size_t)t * kShadowSlot + (addr - sh.addr), size);
+    return XAIE_OK;
+  }
+  if (AieRC rc = issue_pending(d)) return rc;
+  if (size <= kStageBytes) {
+    uint8_t* st = nullptr;
+    if (AieRC rc = stage_take(d, size, &st)) return rc;
+    const bool flagged = size <= kFlagCopyBytes;
+    const uint32_t seq = ++d->stage_seq;
+    stage_copy<<<flagged ? 1u : stage_blocks(size), 256, 0, d->stream>>>(st, d->mem + d->off[t] + addr, size,
+                                                                          flagged ? d->stage_flag : nullptr, seq);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && !(flagged && spin_flag(d->stage_flag, seq))) e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) return hip_fail(d, e, "tile to host copy");
+    std::memcpy(dst, st, size);
+    // Every copy queued before this one has completed (the queue was issued
+    // first, and this copy ran after it), and this one reads no staged bytes,
+    // so the whole buffer is free again.
+    d->stage_used = 0;
+    return XAIE_OK;
+  }
+  const int rc = miaie_copy_d2h(d->ctx, dst, d->mem + d->off[t] + addr, size);
+  return rc ? miaie_fail(d, rc, "tile to host copy") : XAIE_OK;
+}
+
+// XAie_RouteDmaWait: a host -> tile transfer is complete, as far as any
+// caller can tell, once its bytes are staged.  The source buffer may be
+// reused from then on, and every later access to tile memory (a launch, a
+// read, another copy) runs after the device copy in stream order, so there
+// is nothing left to wait for; a queued copy stays queued for the next
+// launch to carry.
+AieRC staged_copies_done(miaie_xaie_dev* d) {
+  (void)d;
+  return XAIE_OK;
+}
+
 // Launch `k` on the tiles in `idx` (all bound to k with the same arg).
 AieRC launch_group(miaie_xaie_dev* d, const XAie_MiaieKernel* k, u32 arg, const std::vector<int>& idx, u32 passes) {
   u32 ping[MIAIE_XAIE_MAX_PARAMS] = {0};
   window_layout(k, ping, nullptr);
+  // A single-tile launch of mm/perf or k1/k2 is fused: it carries the tile's
+  // queued host -> tile copies, mirrors its output window into the tile's
+  // host shadow and publishes its number in the host done flag.  Any other
+  // launch first issues the queued copies.
+  FuseArgs fz{};
+  const bool fusable = idx.size() == 1 && !(k->Flags & MIAIE_XAIE_KERNEL_FOREVER) &&
+                       (k->Builtin == B_MM_NT || k->Builtin == B_K1 || k->Builtin == B_K2);
+  if (fusable) {
+    const int t = idx[0];
+    if (AieRC rc = ensure_stage(d)) return rc;
+    bool mine = d->pend.size() <= (size_t)kFuseCopies;
+    for (const PendCopy& c : d->pend) mine = mine && c.tile == t;
+    if (!mine) {
+      if (AieRC rc = issue_pending(d)) return rc;
+    }
+    for (const PendCopy& c : d->pend) {
+      fz.dst[fz.ncopy] = (u32)c.addr;
+      fz.size[fz.ncopy] = (u32)c.size;
+      fz.src[fz.ncopy] = c.src;
+      ++fz.ncopy;
+    }
+    d->pend.clear();
+    fz.flag = d->done_flag;
+    fz.seq = ++d->fuse_seq;
+    // the output window as declared (size_hint words), at least what the
+    // kernel writes, within the tile's memory
+    const u32 declared = 4 * (k->SizeHint[1] ? k->SizeHint[1] : 512);
+    const u32 out_bytes = std::min(std::max(declared, builtin_extent(k, 1, arg)), d->bytes[t] - ping[1]);
+    if (out_bytes <= kShadowSlot) {
+      fz.shadow = d->shadow_mem + (size_t)t * kShadowSlot;
+      fz.shadow_addr = ping[1];
+      fz.shadow_size = out_bytes;
+      Shadow& sh = d->shadow[t];
+      sh.valid = true;
+      sh.addr = ping[1];
+      sh.size = out_bytes;
+      sh.seq = fz.seq;
+    } else {
+      invalidate_shadow(d, t);
+    }
+    d->cores[t].fused = true;
+    d->cores[t].fused_seq = fz.seq;
+  } else {
+    if (AieRC rc = issue_pending(d)) return rc;
+    for (int t : idx) {
+      invalidate_shadow(d, t);
+      d->cores[t].fused = false;
+    }
+  }
   for (size_t s = 0; s < idx.size(); s += kMaxRunTiles) {
     TileList tl;
     tl.n = (u32)std::min<size_t>(kMaxRunTiles, idx.size() - s);
@@ -343,11 +663,12 @@ AieRC launch_group(miaie_xaie_dev* d, const XAie_MiaieKernel* k, u32 arg, const 
     }
     switch (k->Builtin) {
       case B_MM_NT:
-        tile_mm_nt<<<tl.n, 256, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], (int)arg, passes);
+        tile_mm_nt<<<tl.n, 256, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], (int)arg, passes, fz);
         break;
       case B_K1:
       case B_K2:
-        tile_add20<<<tl.n, 64, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], k->Builtin == B_K2 ? 10 : 1, passes);
+        tile_add20<<<tl.n, 64, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], k->Builtin == B_K2 ? 10 : 1, passes,
+                                               fz);
         break;
       case B_MM3_U64:
         tile_mm3_u64<<<tl.n, 64, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], passes);
@@ -379,8 +700,14 @@ AieRC launch_cores(miaie_xaie_dev* d, const std::vector<int>& tiles, u32 iterati
     const u32 passes = (k->Flags & MIAIE_XAIE_KERNEL_FOREVER) ? MIAIE_XAIE_FOREVER_PASSES : iterations;
     if (AieRC rc = launch_group(d, k, g.first.second, g.second, passes)) return rc;
   }
+  // A lone fused launch signals its completion through the host done flag;
+  // only other batches record an event (a later event's completion also
+  // covers this batch, the numbers being issued in stream order).
   uint64_t seq = 0;
-  if (AieRC rc = record_batch(d, &seq)) return rc;
+  if (tiles.size() == 1 && d->cores[tiles[0]].fused)
+    seq = ++d->issued;
+  else if (AieRC rc = record_batch(d, &seq))
+    return rc;
   for (int t : tiles) {
     d->cores[t].seq = seq;
     d->cores[t].ran = true;
@@ -401,6 +728,8 @@ bool core_done(miaie_xaie_dev* d, int t) {
   const Core& c = d->cores[t];
   if (!c.ran || c.pending) return false;
   if ((c.k->Flags & MIAIE_XAIE_KERNEL_FOREVER) && c.enabled) return false;
+  // a fused launch raises the host done flag itself, ahead of its completion signal
+  if (c.fused && (int32_t)(__atomic_load_n(d->done_flag, __ATOMIC_ACQUIRE) - c.fused_seq) >= 0) return true;
   retire(d);
   return c.seq <= d->completed;
 }
@@ -430,84 +759,6 @@ AieRC tile_range(miaie_xaie_dev* d, int t, uint64_t addr, uint64_t size, const c
   return XAIE_OK;
 }
 
-// Host <-> tile copies up to kStageBytes go through a pinned staging buffer.
-// A host -> tile copy returns once the source bytes are in the staging
-// buffer; the device copy then runs in stream order, ahead of any later
-// launch or copy, as an AIE DMA runs on after XAie_MoveData returns (the
-// perf example waits for it with XAie_RouteDmaWait, aieml_perf.cc:156-163).
-// A tile -> host copy returns once the bytes are in the destination.  Larger
-// copies take the synchronous miaie copies.  Staged host -> tile copies take
-// consecutive slices of the buffer; when it is full, the copies still reading
-// it are waited for and it starts over.
-constexpr size_t kStageBytes = 4u << 20;
-
-AieRC stage_take(miaie_xaie_dev* d, size_t size, uint8_t** slice) {
-  hipError_t e = hipSetDevice(d->device);
-  if (e != hipSuccess) return hip_fail(d, e, "hipSetDevice");
-  if (!d->stage) {
-    e = hipHostMalloc(reinterpret_cast<void**>(&d->stage), kStageBytes, hipHostMallocDefault);
-    if (e != hipSuccess) {
-      d->stage = nullptr;
-      return hip_fail(d, e, "pinned staging buffer");
-    }
-    d->stage_used = 0;
-  }
-  if (!d->stage_ev) {
-    e = hipEventCreateWithFlags(&d->stage_ev, hipEventDisableTiming);
-    if (e != hipSuccess) {
-      d->stage_ev = nullptr;
-      return hip_fail(d, e, "hipEventCreate");
-    }
-  }
-  const size_t need = (size + 255) & ~static_cast<size_t>(255);
-  if (d->stage_used + need > kStageBytes) {
-    e = hipEventSynchronize(d->stage_ev);
-    if (e != hipSuccess) return hip_fail(d, e, "waiting for staged copies");
-    d->stage_used = 0;
-  }
-  *slice = d->stage + d->stage_used;
-  d->stage_used += need;
-  return XAIE_OK;
-}
-
-AieRC copy_h2d(miaie_xaie_dev* d, int t, uint64_t addr, const void* src, size_t size) {
-  if (size == 0) return XAIE_OK;
-  if (size <= kStageBytes) {
-    uint8_t* st = nullptr;
-    if (AieRC rc = stage_take(d, size, &st)) return rc;
-    std::memcpy(st, src, size);
-    hipError_t e = hipMemcpyAsync(d->mem + d->off[t] + addr, st, size, hipMemcpyHostToDevice, d->stream);
-    if (e == hipSuccess) e = hipEventRecord(d->stage_ev, d->stream);
-    return e == hipSuccess ? XAIE_OK : hip_fail(d, e, "host to tile copy");
-  }
-  const int rc = miaie_copy_h2d(d->ctx, d->mem + d->off[t] + addr, src, size);
-  return rc ? miaie_fail(d, rc, "host to tile copy") : XAIE_OK;
-}
-
-AieRC copy_d2h(miaie_xaie_dev* d, int t, uint64_t addr, void* dst, size_t size) {
-  if (size == 0) return XAIE_OK;
-  if (size <= kStageBytes) {
-    uint8_t* st = nullptr;
-    if (AieRC rc = stage_take(d, size, &st)) return rc;
-    hipError_t e = hipMemcpyAsync(st, d->mem + d->off[t] + addr, size, hipMemcpyDeviceToHost, d->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
-    if (e != hipSuccess) return hip_fail(d, e, "tile to host copy");
-    std::memcpy(dst, st, size);
-    d->stage_used = 0;  // the stream has drained: no copy reads the buffer any more
-    return XAIE_OK;
-  }
-  const int rc = miaie_copy_d2h(d->ctx, dst, d->mem + d->off[t] + addr, size);
-  return rc ? miaie_fail(d, rc, "tile to host copy") : XAIE_OK;
-}
-
-// Waits until every staged host -> tile copy has landed.
-AieRC staged_copies_done(miaie_xaie_dev* d) {
-  if (!d->stage_ev) return XAIE_OK;
-  hipError_t e = hipSetDevice(d->device);
-  if (e == hipSuccess) e = hipEventSynchronize(d->stage_ev);
-  return e == hipSuccess ? XAIE_OK : hip_fail(d, e, "waiting for staged copies");
-}
-
 void free_ddr(XAie_MemInst* m) {
   if (m->mapped)
     munmap(m->host, m->mapped);
@@ -533,6 +784,9 @@ void destroy(miaie_xaie_dev* d) {
 
 void reset_state(miaie_xaie_dev* d) {
   for (Core& c : d->cores) c = Core{};
+  for (Shadow& sh : d->shadow) sh = Shadow{};
+  d->pend.clear();  // the stream has drained and the tile memory is cleared
+  d->stage_used = 0;
   for (XAie_RoutingInstance* r : d->routing) r->routes.clear();
 }
 
@@ -591,6 +845,7 @@ MIAIE_XAIE_API AieRC XAie_CfgInitialize(XAie_DevInst* DevInst, const XAie_Config
   d->off.assign(ntiles, 0);
   d->bytes.assign(ntiles, 0);
   d->cores.assign(ntiles, Core{});
+  d->shadow.assign(ntiles, Shadow{});
   size_t total = 0;
   for (u32 c = 0; c < d->cols; ++c)
     for (u32 r = 0; r < d->rows; ++r) {
@@ -735,11 +990,11 @@ MIAIE_XAIE_API AieRC XAie_LoadElfMem(XAie_DevInst* DevInst, XAie_LocType Loc, co
   if (AieRC rc = core_of(d, Loc, "XAie_LoadElfMem", &t)) return rc;
   const XAie_MiaieKernel* k = nullptr;
   if (AieRC rc = valid_kernel(d, ElfMem, &k)) return rc;
-  if (AieRC rc = check_windows(d, k, 16, d->bytes[t])) return rc;
+  if (AieRC rc = check_windows(d, k, window_n(k), d->bytes[t])) return rc;
   if (AieRC rc = flush(d)) return rc;
   Core& c = d->cores[t];
   c.k = k;
-  c.arg = 16;
+  c.arg = window_n(k);
   c.enabled = false;
   c.ran = false;
   return XAIE_OK;
@@ -974,6 +1229,8 @@ MIAIE_XAIE_API AieRC XAie_MoveData(XAie_RoutingInstance* ri, XAie_LocType Source
   if (AieRC rc = tile_range(d, s, src, Size, "XAie_MoveData (source)")) return rc;
   if (AieRC rc = tile_range(d, t, dst, Size, "XAie_MoveData (destination)")) return rc;
   if (Size == 0) return XAIE_OK;
+  if (AieRC rc = issue_pending(d)) return rc;
+  invalidate_shadow(d, t);
   const int rc = miaie_copy_d2d(d->ctx, d->mem + d->off[t] + dst, d->mem + d->off[s] + src, Size);
   return rc ? miaie_fail(d, rc, "XAie_MoveData: tile to tile copy") : XAIE_OK;
 } catch (...) { return out_of_memory(__func__); }
@@ -1153,6 +1410,8 @@ MIAIE_XAIE_API AieRC XAie_WaitOutData(XAie_Kernel_Inst* K) try {
   const int t = tile_index(d, K->loc);
   if (!d->cores[t].ran) return fail(d, XAIE_ERR, "XAie_WaitOutData: kernel %s was not run", K->k->Name);
   if (K->k->Flags & MIAIE_XAIE_KERNEL_FOREVER) d->cores[t].enabled = false;
+  const Core& c = d->cores[t];
+  if (c.fused && spin_flag(d->done_flag, c.fused_seq)) return XAIE_OK;  // its output is in the host shadow
   if (miaie_wait(d->ctx, -1)) return miaie_fail(d, MIAIE_EHIP, "XAie_WaitOutData");
   retire(d);
   return XAIE_OK;
@@ -1224,7 +1483,7 @@ extern "C" MIAIE_XAIE_API AieRC XAie_MiaieRunOnDdr(const XAie_MiaieKernel* Kerne
       int t;
       if (ColStart + c > 255 || RowStart + r > 255) return fail(d, XAIE_INVALID_TILE, "XAie_MiaieRunOnDdr: tile outside");
       if (AieRC rc = core_of(d, loc, "XAie_MiaieRunOnDdr", &t)) return rc;
-      if (AieRC rc = check_windows(d, k, 16, d->bytes[t])) return rc;
+      if (AieRC rc = check_windows(d, k, window_n(k), d->bytes[t])) return rc;
       tiles.push_back(t);
     }
   if (AieRC rc = flush(d)) return rc;
@@ -1232,7 +1491,7 @@ extern "C" MIAIE_XAIE_API AieRC XAie_MiaieRunOnDdr(const XAie_MiaieKernel* Kerne
     if (AieRC rc = copy_h2d(d, t, ping[0], reinterpret_cast<const void*>((uintptr_t)InAddr), in_bytes)) return rc;
     Core& c = d->cores[t];
     c.k = k;
-    c.arg = 16;
+    c.arg = window_n(k);
     c.reset = false;
     c.enabled = true;
   }

@@ -7,6 +7,8 @@
  * exits 0 on a match:
  *   mm [reps]     example/matrixmultiply/aieml_mm.cc:108-249 (+ main :251-296),
  *                 timed over the span aieml_mm.cc:148-190 times
+ *   mm8 [reps]    the same flow for the program's 8x8 build (MAT_SIZE 64),
+ *                 the "15us(8*8)" case aieml_mm.cc:257 prints
  *   perf [reps]   example/perf/aieml_perf.cc:105-254, partitioned at column 2
  *   multi_tile    example/multi/multi_tile.cpp:65-181 (expects 26)
  *   seq_full_col  example/multi/seq_full_col.cpp:65-181 (expects 23)
@@ -97,10 +99,11 @@ static void wait_core(XAie_DevInst* dev, XAie_LocType loc) {
     }
 }
 
-/* aieml_mm.cc / aieml_perf.cc: one 16x16 NT tile through DDR -> tile -> DDR. */
-static int flow_window(const XAie_MiaieKernel* kernel, int startcol, int ncols, int shimcol, int first_value,
+/* aieml_mm.cc / aieml_perf.cc: one n x n NT tile (n = 16, or 8 for the
+ * MAT_SIZE 64 build of aieml_mm.cc) through DDR -> tile -> DDR. */
+static int flow_window(const XAie_MiaieKernel* kernel, int N, int startcol, int ncols, int shimcol, int first_value,
                        int use_ext_calls, int reps) {
-  enum { N = 16, MAT_SIZE = N * N };
+  const int MAT_SIZE = N * N;
   XAie_DevInst dev;
   open_device(&dev, startcol, ncols);
   const XAie_LocType core = XAie_TileLoc(4, 4), shim = XAie_TileLoc((u8)shimcol, 0);
@@ -160,7 +163,7 @@ static int flow_window(const XAie_MiaieKernel* kernel, int startcol, int ncols, 
 
   const int bad = golden_mismatches((const int32_t*)XAie_MemGetVAddr(in), (const int32_t*)XAie_MemGetVAddr(out), N);
   const int32_t* o = (const int32_t*)XAie_MemGetVAddr(out);
-  printf("C[0][0] = %d, C[15][15] = %d\n", o[0], o[MAT_SIZE - 1]);
+  printf("C[0][0] = %d, C[%d][%d] = %d\n", o[0], N - 1, N - 1, o[MAT_SIZE - 1]);
   if (bad == 0)
     printf("%s: CPU result matches the device output.\n", kernel->Name);
   else
@@ -416,15 +419,17 @@ static int flow_errors(void) {
 
 int main(int argc, char** argv) {
   if (argc < 2) {
-    fprintf(stderr, "usage: %s mm [reps]|perf [reps]|multi_tile|seq_full_col|vek385 [cols]|oob|errors\n", argv[0]);
+    fprintf(stderr, "usage: %s mm [reps]|mm8 [reps]|perf [reps]|multi_tile|seq_full_col|vek385 [cols]|oob|errors\n",
+            argv[0]);
     return 64;
   }
   const char* cmd = argv[1];
   const int reps = argc > 2 ? atoi(argv[2]) : 1;
-  if (!strcmp(cmd, "mm") || !strcmp(cmd, "perf")) {
+  if (!strcmp(cmd, "mm") || !strcmp(cmd, "mm8") || !strcmp(cmd, "perf")) {
     if (reps < 1 || reps > 100000) return 64;
-    if (!strcmp(cmd, "mm")) return flow_window(&miaie_xaie_mm, 0, 0, 2, 0, 0, reps);   /* aieml_mm.cc:137-140 */
-    return flow_window(&miaie_xaie_perf, 2, 34, 33, 1, 1, reps);                      /* aieml_perf.cc:141-144 */
+    if (!strcmp(cmd, "mm")) return flow_window(&miaie_xaie_mm, 16, 0, 0, 2, 0, 0, reps);  /* aieml_mm.cc:137-140 */
+    if (!strcmp(cmd, "mm8")) return flow_window(&miaie_xaie_mm8, 8, 0, 0, 2, 0, 0, reps); /* aieml_mm.cc:257, 8x8 */
+    return flow_window(&miaie_xaie_perf, 16, 2, 34, 33, 1, 1, reps);                      /* aieml_perf.cc:141-144 */
   }
   if (!strcmp(cmd, "multi_tile")) return flow_multi_tile();
   if (!strcmp(cmd, "seq_full_col")) return flow_seq_full_col();

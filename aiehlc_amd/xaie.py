@@ -146,7 +146,7 @@ SIGS = {
     "XAie_KernelFree": (_rc, [_p]),
     "XAie_MiaieRunOnDdr": (_rc, [C.POINTER(Kernel), _u32, _u32, _u32, _u32, _u64, _u64]),
 }
-BUILTINS = ("miaie_xaie_mm", "miaie_xaie_perf", "miaie_xaie_k1", "miaie_xaie_k2", "miaie_xaie_mm3_u64",
+BUILTINS = ("miaie_xaie_mm", "miaie_xaie_mm8", "miaie_xaie_perf", "miaie_xaie_k1", "miaie_xaie_k2", "miaie_xaie_mm3_u64",
             "miaie_xaie_perf_u8")
 
 _lib = None

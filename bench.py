@@ -19,10 +19,11 @@ Also in the line (not the headline):
                          conv's and the GEMM's grid and LDS size
                          (aiehlc_amd/probes/launch_floor); the conv line carries
                          its own floor and the time above it
-  extras.reference_flow_16x16  the reference's own timed example flow
-                         (aieml_mm.cc: 16x16 int32 tile moved in, run, waited
-                         for, moved out) through the aie-rt facade, beside the
-                         215 us the reference prints for it
+  extras.reference_flow_16x16, extras.reference_flow_8x8
+                         the reference's own timed example flow (aieml_mm.cc:
+                         an int32 tile moved in, run, waited for, moved out)
+                         through the aie-rt facade, beside the 215 us (16x16)
+                         and 15 us (8x8) the reference prints for it
   extras.vendor_library  the same int8 4096^3 and bf16 8192^3 products through
                          hipBLASLt (torch._int_mm / torch.matmul) on this GPU
   cpu_baseline           the reference's CPU golden loop (i-j-k, int32
@@ -257,27 +258,28 @@ def mfma_ceiling() -> dict | None:
     return probe_json(CEILING_EXE)
 
 
-def reference_flow(reps: int = 500) -> dict | None:
+def reference_flow(sub: str = "mm", n: int = 16, expected_us: float = 215.0, reps: int = 500) -> dict | None:
     """The reference's own timed example: aieml_mm.cc's XAie_* sequence
     (move A||B into the tile, run, wait for done, move C out, MemSyncForCPU;
-    the span its stopwatch covers, :148-190) for the 16x16 int32 NT tile,
+    the span its stopwatch covers, :148-190) for an n x n int32 NT tile,
     through the aie-rt facade on this GPU.  The reference prints that this
-    span "should be 215 us" for 16x16 on its AIE-ML board (aieml_mm.cc:257)."""
+    span "should be 15us(8*8) 215 us(16*16)" on its AIE-ML board
+    (aieml_mm.cc:257)."""
     if not os.path.exists(FLOWS_EXE):
         return None
-    r = subprocess.run([FLOWS_EXE, "mm", str(reps)], capture_output=True, text=True, timeout=120)
+    r = subprocess.run([FLOWS_EXE, sub, str(reps)], capture_output=True, text=True, timeout=120)
     m = re.search(r"median over (\d+) runs: ([0-9.]+) us \(min ([0-9.]+) us\)", r.stdout)
     first = re.search(r"Output took ([0-9.]+) us", r.stdout)
     if r.returncode != 0 or not m:
         return {"error": (r.stdout + r.stderr).strip()[-300:]}
     med = float(m.group(2))
-    return {"flow": "aieml_mm.cc 16x16 int32 NT: XAie_MoveData in, XAie_Run, XAie_CoreWaitForDone, XAie_MoveData out, "
-                    "XAie_MemSyncForCPU (aiehlc_amd/harness/xaie_flows mm)",
+    return {"flow": f"aieml_mm.cc {n}x{n} int32 NT: XAie_MoveData in, XAie_Run, XAie_CoreWaitForDone, XAie_MoveData out, "
+                    f"XAie_MemSyncForCPU (aiehlc_amd/harness/xaie_flows {sub})",
             "median_us": med, "min_us": float(m.group(3)), "first_us": float(first.group(1)) if first else None,
             "runs": int(m.group(1)),
-            "reference_expected_us": 215.0,
+            "reference_expected_us": expected_us,
             "reference_expected_source": "aieml_mm.cc:257 (printed expectation on VEK280 AIE-ML with caches on)",
-            "speedup_vs_reference_expected": round(215.0 / med, 2)}
+            "speedup_vs_reference_expected": round(expected_us / med, 2)}
 
 
 def vendor_library(steps: int) -> dict:
@@ -474,6 +476,7 @@ def main() -> int:
     if not args.no_extras:
         extras["mfma_ceiling"] = mfma_ceiling()
         extras["reference_flow_16x16"] = reference_flow()
+        extras["reference_flow_8x8"] = reference_flow("mm8", 8, 15.0)
         floor = probe_json(FLOOR_EXE)
         extras["launch_floor"] = floor
         conv = extras.get("conv2d_3x3")

@@ -191,6 +191,7 @@ typedef struct {
  * harness swaps its kernel definition for e.g. `#define mm (&miaie_xaie_mm)`
  * and keeps `XAie_LoadElfMem(dev, loc, (unsigned char *)mm)`. */
 MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_mm;     /* aieml_mm.cc:41-93: int32 16x16 NT, in 0x1000, out 0x6000 */
+MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_mm8;    /* the same kernel built for 8x8 (MAT_SIZE 64, the "15us(8*8)" case of aieml_mm.cc:257): size_hint 128 */
 MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_perf;   /* aieml_perf.cc:61-83: uint32 16x16 NT at DM 0x1000 -> 0x6000 */
 MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_k1;     /* multi_tile.cpp:39-42: out[0..20) = in[0] + 1 */
 MIAIE_XAIE_API extern const XAie_MiaieKernel miaie_xaie_k2;     /* multi_tile.cpp:44-47: out[0..20) = in[0] + 10 */
@@ -317,7 +318,10 @@ MIAIE_XAIE_API AieRC XAie_MoveDataExternal2Aie(XAie_RoutingInstance* RoutingInst
 /* Tile memory at SrcAddr -> DDR buffer (multi_tile.cpp:148-150). */
 MIAIE_XAIE_API AieRC XAie_MoveDataAie2External(XAie_RoutingInstance* RoutingInstance, XAie_LocType Source, u64 SrcAddr,
                                                u32 Size, XAie_MemInst* MemInst, XAie_LocType Destination);
-/* Moves are complete on return; this only checks the route (aieml_perf.cc:163). */
+/* Checks the route (aieml_perf.cc:163).  Moves out of a tile are complete on
+ * return; a move into a tile counts as complete once its bytes are staged
+ * (every later access to tile memory is ordered after the device copy), so
+ * there is nothing left to wait for. */
 MIAIE_XAIE_API AieRC XAie_RouteDmaWait(XAie_RoutingInstance* RoutingInstance, XAie_LocType Source,
                                        XAie_LocType Destination, u8 IsMm2s);
 /* XAie_Run(ri, 1) (aieml_mm.cc:167): run every loaded, out-of-reset core on

@@ -120,6 +120,7 @@ FLOWS = [
     # (args, lines the output must hold): the known answers are the reference's own
     (["mm"], ["C[0][0] = 31960, C[15][15] = 1994200", "CPU result matches"]),     # aieml_mm.cc:137-140
     (["mm", "50"], ["C[0][0] = 31960, C[15][15] = 1994200", "CPU result matches", "median over 50 runs"]),
+    (["mm8", "20"], ["C[0][0] = 1932, C[7][7] = 58828", "CPU result matches"]),   # the 8x8 build; aieoob.c:83-86 values
     (["perf"], ["C[0][0] = 36312, C[15][15] = 2006232", "CPU result matches"]),   # aieml_perf.cc:141-144
     (["perf", "20"], ["C[0][0] = 36312, C[15][15] = 2006232", "CPU result matches", "median over 20 runs"]),
     (["multi_tile"], ["out[0] = 26 (expected 26), 0 mismatches"]),                # multi_tile.cpp:150
@@ -236,3 +237,89 @@ def test_partition_columns_are_relative():
         assert dev.lib.XAie_MiaieTileMemBytes(dev.ref, X.tile(33, 4)) == 64 << 10
         assert dev.lib.XAie_MiaieTileMemBytes(dev.ref, X.tile(34, 4)) == 0
         assert dev.call("CoreReset", X.tile(34, 4)) == X.XAIE_INVALID_TILE
+
+
+def _mm_nt(win: np.ndarray, n: int = 16) -> np.ndarray:
+    """The mm kernel's result on an A||B window (aieml_mm.cc:194-230): out[i][j]
+    = sum_k A[i][k] * B[j][k] in 32-bit wrap-around arithmetic."""
+    a = win[: n * n].reshape(n, n).astype(np.uint64)
+    b = win[n * n: 2 * n * n].reshape(n, n).astype(np.uint64)
+    return ((a @ b.T) % (1 << 32)).astype(np.uint32).reshape(-1)
+
+
+@pytest.mark.gpu
+def test_fused_launch_ordering():
+    """A single-tile mm launch carries its tile's staged moves and mirrors its
+    output window to the host.  Every path that could see stale data: a write
+    into the mirrored window, more staged moves than one launch carries, a
+    staged move for another tile, a read before any launch, a tile-to-tile
+    move into the window, back-to-back runs, and XAie_RouteDmaWait."""
+    mm = X.builtin("miaie_xaie_mm")
+    rng = np.random.default_rng(11)
+    with X.Device() as dev:
+        core, core2, shim = X.tile(4, 4), X.tile(6, 4), X.tile(2, 0)
+        for c in (core, core2):
+            dev.check(dev.call("CoreReset", c))
+            dev.check(dev.call("CoreUnreset", c))
+            dev.check(dev.call("LoadElfMem", c, C.cast(C.pointer(mm), C.c_void_p)))
+        # one routing instance per core, so that XAie_Run launches one tile
+        # (the fused form); a third one for the tile-to-tile move
+        ri_a, ri_b, ri_c = (dev.lib.XAie_InitRoutingHandler(dev.ref) for _ in range(3))
+        dev.check(dev.lib.XAie_Route(ri_a, None, shim, core))
+        dev.check(dev.lib.XAie_Route(ri_b, None, shim, core2))
+        dev.check(dev.lib.XAie_Route(ri_c, None, core, core2))
+
+        def write(t, addr, arr):
+            dev.check(dev.call("DataMemBlockWrite", t, addr, arr.ctypes.data, arr.nbytes))
+
+        def read(t, addr, nwords):
+            got = np.zeros(nwords, np.uint32)
+            dev.check(dev.call("DataMemBlockRead", t, addr, got.ctypes.data, got.nbytes))
+            return got
+
+        def run(ri, c):
+            dev.check(dev.lib.XAie_Run(ri, 1))
+            dev.check(dev.call("CoreWaitForDone", c, 1_000_000))
+
+        # 1. the staged move rides in the launch; the result comes from the mirror
+        w1 = rng.integers(0, 2**32, 512, dtype=np.uint32)
+        w2 = rng.integers(0, 2**32, 512, dtype=np.uint32)
+        write(core, 0x1000, w1)
+        write(core2, 0x1000, w2)  # a staged move for another tile: both are issued before the launch
+        run(ri_a, core)
+        run(ri_b, core2)
+        np.testing.assert_array_equal(read(core, 0x6000, 256), _mm_nt(w1))
+        np.testing.assert_array_equal(read(core2, 0x6000, 256), _mm_nt(w2))
+        # 2. a write into the mirrored window makes the mirror stale
+        patch = np.full(4, 0xABABABAB, np.uint32)
+        write(core, 0x6000 + 64, patch)
+        want = _mm_nt(w1)
+        want[16:20] = patch
+        np.testing.assert_array_equal(read(core, 0x6000, 256), want)
+        # 3. more staged moves than one launch carries (8 pieces of 256 B), and a
+        #    read of the input window before any launch
+        w3 = rng.integers(0, 2**32, 512, dtype=np.uint32)
+        for p in range(8):
+            write(core, 0x1000 + 256 * p, w3[64 * p: 64 * (p + 1)])
+        np.testing.assert_array_equal(read(core, 0x1000, 512), w3)
+        w4 = rng.integers(0, 2**32, 512, dtype=np.uint32)
+        for p in range(8):
+            write(core, 0x1000 + 256 * p, w4[64 * p: 64 * (p + 1)])
+        dev.check(dev.lib.XAie_RouteDmaWait(ri_a, shim, core, 1))
+        run(ri_a, core)
+        np.testing.assert_array_equal(read(core, 0x6000, 256), _mm_nt(w4))
+        np.testing.assert_array_equal(read(core2, 0x6000, 256), _mm_nt(w2))
+        # 4. a tile-to-tile move into core2's mirrored output window
+        dev.check(dev.lib.XAie_MoveData(ri_c, core, C.c_void_p(0x1000), 256, C.c_void_p(0x6000), core2))
+        want2 = _mm_nt(w2)
+        want2[:64] = w4[:64]
+        np.testing.assert_array_equal(read(core2, 0x6000, 256), want2)
+        # 5. back-to-back runs with new inputs and no read in between
+        for _ in range(3):
+            w5 = rng.integers(0, 2**32, 512, dtype=np.uint32)
+            write(core, 0x1000, w5)
+            run(ri_a, core)
+        np.testing.assert_array_equal(read(core, 0x6000, 256), _mm_nt(w5))
+        done = C.c_uint8()
+        dev.check(dev.call("CoreReadDoneBit", core, C.byref(done)))
+        assert done.value == 1
