@@ -88,14 +88,20 @@ __device__ void fuse_out(uint8_t* base, const FuseArgs& f) {
 // window holds A[n][n] then B as [n][k] (n*n words each); out[i][j] =
 // sum_k A[i][k] * B[j][k] in 32-bit wrap-around arithmetic.  n <= 16, so one
 // workgroup of 256 lanes covers a tile's whole output.
+// The window is read from tile memory into LDS once, all words in flight
+// together, so the k-loop does not wait on a global load per step.
 __global__ __launch_bounds__(256) void tile_mm_nt(uint8_t* __restrict__ mem, TileList tl, u32 in_addr, u32 out_addr,
                                                   int n, u32 passes, FuseArgs fz) {
+  __shared__ uint32_t win[2 * 16 * 16];
   uint8_t* base = mem + tl.off[blockIdx.x];
   fuse_in(base, fz);
-  const uint32_t* a = reinterpret_cast<const uint32_t*>(base + in_addr);
-  const uint32_t* bt = a + n * n;
-  uint32_t* out = reinterpret_cast<uint32_t*>(base + out_addr);
+  const uint32_t* in = reinterpret_cast<const uint32_t*>(base + in_addr);
   const int t = threadIdx.x;
+  for (int w = t; w < 2 * n * n; w += blockDim.x) win[w] = in[w];
+  __syncthreads();
+  const uint32_t* a = win;
+  const uint32_t* bt = win + n * n;
+  uint32_t* out = reinterpret_cast<uint32_t*>(base + out_addr);
   if (t < n * n) {
     const int i = t / n, j = t - i * n;
     for (u32 p = 0; p < passes; ++p) {
