@@ -201,10 +201,14 @@ MIAIE_API int miaie_gemm_bf16_f32(miaie_ctx* ctx, const uint16_t* A, const uint1
 
 /* int8 conv2d, NHWC activations X[N][H][W][Cin], OHWI weights
  * W[Cout][R][S][Cin], zero padding, stride, per-output-channel requant
- * Y = sat_int8((acc + 2^(s_c-1)) >> s_c) with s_c = shifts[c] in [0, 31],
- * Y[N][Ho][Wo][Cout] with Ho = (H + 2*pad - R)/stride + 1 (Wo alike).
- * Implemented: Cin and Cout multiples of 32, Cin <= 256, Cout <= 256; other
- * channel counts return MIAIE_EUNSUPPORTED. */
+ * Y = sat_int8((acc + 2^(s_c-1)) >> s_c) with s_c = shifts[c] in [0, 31]
+ * (a device array the library cannot check: other values give unspecified
+ * results), Y[N][Ho][Wo][Cout] with Ho = (H + 2*pad - R)/stride + 1 (Wo
+ * alike).  Any shape: 3x3 stride-1 convolutions with Cin 32 or 64, Cout a
+ * multiple of 32 and Wo <= 64 take the row-block kernel; Cin a multiple of
+ * 32 with Cout a multiple of 64 the implicit-GEMM kernel; everything else a
+ * direct kernel.
+ * R*S*Cin above 2^30 or N*H*W*Cin above 2^40 return MIAIE_EINVAL. */
 MIAIE_API int miaie_conv2d_i8_nhwc(miaie_ctx* ctx, const int8_t* X, const int8_t* W,
                                    const uint8_t* shifts, int8_t* Y, int N, int H, int W_, int Cin,
                                    int Cout, int R, int S, int stride, int pad);
