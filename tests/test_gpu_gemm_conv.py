@@ -110,7 +110,8 @@ def test_gemm_i8_rq_without_debug_output(ctx):
 def test_gemm_i8_rq_4096_config(ctx):
     """Config 2: M=N=K=4096 NN, shift 10.  Bit-exact on a row slab plus 64
     scattered rows; the int8 output must be the requant of the int32 output
-    everywhere; linearity in A checks every element."""
+    everywhere; linearity in A and a row permutation of A check every
+    element."""
     M = N = K = 4096
     _say("gemm_i8_rq 4096^3")
     A = synth.int8((M, K), 1)
@@ -123,8 +124,13 @@ def test_gemm_i8_rq_4096_config(ctx):
     rows = np.random.default_rng(0).choice(np.arange(256, M), size=64, replace=False)
     Cr = oracle.gemm_i8(A[rows], B)
     assert np.array_equal(Cg[rows], Cr)
-    # full-size property: C(A) - C(A with row-block permuted) ... linearity:
-    # C(2*A') where A' = A>>1 equals 2*C(A'), every element (int8 range kept)
+    # full-size properties, every element: the Y-only kernel (the benchmarked
+    # one) on a row permutation of A gives the permuted Y of the Y + C run
+    # above; linearity, C(2*A') = 2*C(A') with A' = A>>1 (int8 range kept)
+    perm = np.random.default_rng(4).permutation(M)
+    Yp, _ = _run_gemm_i8(ctx, np.ascontiguousarray(A[perm]), B, mi.B_NN, 10, False, want_c=False)
+    assert np.array_equal(Yp, Yg[perm])
+    del Yp
     Ah = (A >> 1).astype(np.int8)
     _, Ch = _run_gemm_i8(ctx, Ah, B, mi.B_NN)
     _, Ch2 = _run_gemm_i8(ctx, (Ah * 2).astype(np.int8), B, mi.B_NN)
@@ -316,7 +322,10 @@ def test_mlp_i8(ctx, shape):
 
 def test_mlp_i8_config(ctx):
     """Config 5: X 2048x4096 -> W1 4096x11008 (rq 11 + ReLU) -> W2 11008x4096 (rq 12).
-    Bit-exact H and Y on a 64-row slab and 32 scattered rows."""
+    Bit-exact H and Y on a 64-row slab and 32 scattered rows against the
+    oracle; over all rows, a row permutation of X permutes H and Y exactly
+    (each output row depends on its own input row only, so a result that
+    depends on where a row lands in the tile grid shows up here)."""
     M, K, F, Nout = 2048, 4096, 11008, 4096
     _say("mlp config 5")
     X = synth.int8((M, K), 3)
@@ -327,6 +336,12 @@ def test_mlp_i8_config(ctx):
     ctx.mlp_i8(dX, d1, d2, dH, dY, M, K, F, Nout, 11, 12)
     ctx.wait(120_000)
     Hg, Yg = ctx.download(dH), ctx.download(dY)
+    perm = np.random.default_rng(5).permutation(M)
+    ctx.copy_h2d(dX, np.ascontiguousarray(X[perm]))
+    ctx.mlp_i8(dX, d1, d2, dH, dY, M, K, F, Nout, 11, 12)
+    ctx.wait(120_000)
+    assert np.array_equal(ctx.download(dH), Hg[perm])
+    assert np.array_equal(ctx.download(dY), Yg[perm])
     for b in (dX, d1, d2, dH, dY):
         b.free()
     assert Hg.min() >= 0  # ReLU
