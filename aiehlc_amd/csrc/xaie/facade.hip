@@ -690,7 +690,13 @@ AieRC launch_group(miaie_xaie_dev* d, const XAie_MiaieKernel* k, u32 arg, const 
         break;
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(d, e, k->Name ? k->Name : "tile kernel");
+    if (e != hipSuccess) {
+      for (int t : idx) {  // nothing will fill the shadow or raise the flag
+        invalidate_shadow(d, t);
+        d->cores[t].fused = false;
+      }
+      return hip_fail(d, e, k->Name ? k->Name : "tile kernel");
+    }
   }
   return XAIE_OK;
 }
