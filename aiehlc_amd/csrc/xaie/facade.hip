@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstddef>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -30,7 +31,7 @@ namespace {
 constexpr u32 kCoreMemAie1 = 32u << 10;   // AIE1 core tile data memory
 constexpr u32 kCoreMem = 64u << 10;       // AIE-ML / AIE2PS core tile data memory
 constexpr u32 kMemTileMem = 512u << 10;   // memory tile
-constexpr u32 kMaxRunTiles = 500;         // tiles in one launch (kernel argument block)
+constexpr u32 kMaxRunTiles = 320;         // tiles in one launch (kernel argument block; a 38x8 array of cores fits)
 constexpr u32 kDefaultWaitUs = 500;
 
 enum Builtin : u32 { B_NONE = 0, B_MM_NT = 1, B_K1 = 2, B_K2 = 3, B_MM3_U64 = 4, B_DOT_U8 = 5 };
@@ -47,16 +48,24 @@ struct TileList {
 // run in the kernel's prologue (reading the pinned staging buffer over PCIe),
 // the output window is copied to the host shadow in its epilogue, and `seq`
 // is published in a host flag once both are there.
+// Copies whose bytes fit kFuseInline travel inside the kernel arguments
+// (which the runtime places in device memory) instead of being read from
+// the pinned staging buffer over PCIe; the whole argument block (tile list,
+// these, the scalars) stays under 4 KiB.
 constexpr int kFuseCopies = 4;
+constexpr u32 kFuseInline = 2048;
+constexpr u32 kNotInline = ~0u;
 struct FuseArgs {
   u32 ncopy;
   u32 dst[kFuseCopies];              // tile-relative byte offsets
   u32 size[kFuseCopies];
-  const uint8_t* src[kFuseCopies];   // pinned staging
+  u32 inl_off[kFuseCopies];          // offset of the bytes in inl, or kNotInline
+  const uint8_t* src[kFuseCopies];   // pinned staging (copies not inline)
   uint8_t* shadow;                   // pinned host mirror of the output window, or null
   u32 shadow_addr, shadow_size;
   uint32_t* flag;                    // host word that receives seq, or null
   uint32_t seq;
+  alignas(16) uint8_t inl[kFuseInline];
 };
 
 __device__ void block_copy(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, u32 n) {
@@ -69,9 +78,42 @@ __device__ void block_copy(uint8_t* __restrict__ dst, const uint8_t* __restrict_
   }
 }
 
-__device__ void fuse_in(uint8_t* base, const FuseArgs& f) {
-  for (u32 c = 0; c < f.ncopy; ++c) block_copy(base + f.dst[c], f.src[c], f.size[c]);
+// `inl` points at f.inl where the kernel argument segment holds it (read in
+// place: indexing the by-value argument itself would copy it to scratch).
+__device__ void fuse_in(uint8_t* base, const FuseArgs& f, const uint8_t* inl) {
+#pragma unroll
+  for (int c = 0; c < kFuseCopies; ++c)
+    if ((u32)c < f.ncopy)
+      block_copy(base + f.dst[c], f.inl_off[c] != kNotInline ? inl + f.inl_off[c] : f.src[c], f.size[c]);
   __syncthreads();
+}
+
+// The tile kernels take one argument block each, so the argument segment
+// starts with it and its inline bytes sit at a fixed offset.
+struct MmArgs {
+  uint8_t* mem;
+  TileList tl;
+  u32 in_addr, out_addr;
+  int n;
+  u32 passes;
+  FuseArgs fz;
+};
+struct AddArgs {
+  uint8_t* mem;
+  TileList tl;
+  u32 in_addr, out_addr;
+  int addend;
+  u32 passes;
+  FuseArgs fz;
+};
+template <typename Args>
+__device__ __forceinline__ const uint8_t* kernarg_inline() {
+#if __HIP_DEVICE_COMPILE__  // the builtin exists in the device pass only
+  return reinterpret_cast<const uint8_t*>(__builtin_amdgcn_kernarg_segment_ptr()) + offsetof(Args, fz) +
+         offsetof(FuseArgs, inl);
+#else
+  return nullptr;
+#endif
 }
 
 __device__ void fuse_out(uint8_t* base, const FuseArgs& f) {
@@ -90,11 +132,13 @@ __device__ void fuse_out(uint8_t* base, const FuseArgs& f) {
 // workgroup of 256 lanes covers a tile's whole output.
 // The window is read from tile memory into LDS once, all words in flight
 // together, so the k-loop does not wait on a global load per step.
-__global__ __launch_bounds__(256) void tile_mm_nt(uint8_t* __restrict__ mem, TileList tl, u32 in_addr, u32 out_addr,
-                                                  int n, u32 passes, FuseArgs fz) {
+__global__ __launch_bounds__(256) void tile_mm_nt(MmArgs args) {
+  const u32 in_addr = args.in_addr, out_addr = args.out_addr, passes = args.passes;
+  const int n = args.n;
+  const FuseArgs& fz = args.fz;
   __shared__ uint32_t win[2 * 16 * 16];
-  uint8_t* base = mem + tl.off[blockIdx.x];
-  fuse_in(base, fz);
+  uint8_t* base = args.mem + args.tl.off[blockIdx.x];
+  fuse_in(base, fz, kernarg_inline<MmArgs>());
   const uint32_t* in = reinterpret_cast<const uint32_t*>(base + in_addr);
   const int t = threadIdx.x;
   for (int w = t; w < 2 * n * n; w += blockDim.x) win[w] = in[w];
@@ -115,10 +159,12 @@ __global__ __launch_bounds__(256) void tile_mm_nt(uint8_t* __restrict__ mem, Til
 
 // `k1` / `k2` (multi_tile.cpp:39-47, seq_full_col.cpp:39-47): 20 words of
 // out = in[0] + addend.
-__global__ __launch_bounds__(64) void tile_add20(uint8_t* __restrict__ mem, TileList tl, u32 in_addr, u32 out_addr,
-                                                 int addend, u32 passes, FuseArgs fz) {
-  uint8_t* base = mem + tl.off[blockIdx.x];
-  fuse_in(base, fz);
+__global__ __launch_bounds__(64) void tile_add20(AddArgs args) {
+  const u32 in_addr = args.in_addr, out_addr = args.out_addr, passes = args.passes;
+  const int addend = args.addend;
+  const FuseArgs& fz = args.fz;
+  uint8_t* base = args.mem + args.tl.off[blockIdx.x];
+  fuse_in(base, fz, kernarg_inline<AddArgs>());
   const int32_t* in = reinterpret_cast<const int32_t*>(base + in_addr);
   int32_t* out = reinterpret_cast<int32_t*>(base + out_addr);
   if (threadIdx.x < 20)
@@ -624,10 +670,18 @@ AieRC launch_group(miaie_xaie_dev* d, const XAie_MiaieKernel* k, u32 arg, const 
     if (!mine) {
       if (AieRC rc = issue_pending(d)) return rc;
     }
+    u32 inl_used = 0;
     for (const PendCopy& c : d->pend) {
       fz.dst[fz.ncopy] = (u32)c.addr;
       fz.size[fz.ncopy] = (u32)c.size;
       fz.src[fz.ncopy] = c.src;
+      fz.inl_off[fz.ncopy] = kNotInline;
+      if (c.size <= kFuseInline - inl_used) {
+        std::memcpy(fz.inl + inl_used, c.src, c.size);
+        fz.inl_off[fz.ncopy] = inl_used;
+        inl_used += (u32)((c.size + 15) & ~static_cast<size_t>(15));
+        if (inl_used > kFuseInline) inl_used = kFuseInline;
+      }
       ++fz.ncopy;
     }
     d->pend.clear();
@@ -669,12 +723,12 @@ AieRC launch_group(miaie_xaie_dev* d, const XAie_MiaieKernel* k, u32 arg, const 
     }
     switch (k->Builtin) {
       case B_MM_NT:
-        tile_mm_nt<<<tl.n, 256, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], (int)arg, passes, fz);
+        tile_mm_nt<<<tl.n, 256, 0, d->stream>>>(MmArgs{d->mem, tl, ping[0], ping[1], (int)arg, passes, fz});
         break;
       case B_K1:
       case B_K2:
-        tile_add20<<<tl.n, 64, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], k->Builtin == B_K2 ? 10 : 1, passes,
-                                               fz);
+        tile_add20<<<tl.n, 64, 0, d->stream>>>(
+            AddArgs{d->mem, tl, ping[0], ping[1], k->Builtin == B_K2 ? 10 : 1, passes, fz});
         break;
       case B_MM3_U64:
         tile_mm3_u64<<<tl.n, 64, 0, d->stream>>>(d->mem, tl, ping[0], ping[1], passes);
