@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
 }
 
 // Row-block kernel for stride-1 convolutions with Wo <= 64 (instantiated for
-// 3x3 filters and Cin in {32, 64}).  A workgroup owns ROWS output rows of one
+// 3x3 filters and Cin in {32, 64, 128}).  A workgroup owns ROWS output rows of one
 // image (64 columns, padded) and one block of WCO output channels, with
 // ROWS * WCO = 128 so that its 8 waves each own 32 pixels x 32 channels.  It
 // stages in LDS once, with every global load of the staging in flight
@@ -189,7 +189,7 @@ struct RowsGeom {
   static constexpr int X_BYTES = XR * XC * CIN;
   static constexpr int LDS = X_BYTES + WCO * WP;
   static constexpr int T = R * S * CIN / 32;                // 32-wide k-steps
-  static_assert(LDS <= 65536, "row-block conv LDS budget");
+  static_assert(LDS <= 163840, "row-block conv LDS budget (160 KiB per workgroup on gfx950)");
 };
 
 template <int R, int S, int CIN, int ROWS, int WCO>
@@ -365,9 +365,9 @@ void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, const uint
 
 namespace miaie {
 
-// Row-block shape: 4 output rows x 32 channels stages fewer bytes per
-// workgroup (X 6 rows + W 32 rows) than 2 rows x 64 channels (X 4 rows + W 64
-// rows) when Cout is not a multiple of 64 or the weights dominate.
+// Row-block shape: 2 output rows x 64 channels when Cout is a multiple of 64;
+// 4 rows x 32 channels (smaller staging, but the staging is bound by load
+// latency, not bytes, and it measured slower at 64 channels) otherwise.
 template <int CIN>
 static int launch_rows(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
                        int H, int Wd, int Cout, int pad, int Ho, int Wo) {
@@ -384,11 +384,12 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
   const int Wo = (Wd + 2 * pad - S) / stride + 1;
   const size_t P = (size_t)N * Ho * Wo;
   // Row-block kernel (3x3, stride 1, Cin 32 or 64, Wo <= 64).
-  const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64) && Cout % 32 == 0 &&
+  const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64 || Cin == 128) && Cout % 32 == 0 &&
                        Wo <= PB && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) && aligned(shifts, 4) &&
                        N <= 65535 && (size_t)N * H * Wd * Cin < ((size_t)1 << 31) &&
                        (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31);
   if (rows_ok) {
+    if (Cin == 128) return launch_rows<128>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
     if (Cin == 64) return launch_rows<64>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
     return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
   }

@@ -204,7 +204,7 @@ MIAIE_API int miaie_gemm_bf16_f32(miaie_ctx* ctx, const uint16_t* A, const uint1
  * Y = sat_int8((acc + 2^(s_c-1)) >> s_c) with s_c = shifts[c] in [0, 31]
  * (a device array the library cannot check: other values give unspecified
  * results), Y[N][Ho][Wo][Cout] with Ho = (H + 2*pad - R)/stride + 1 (Wo
- * alike).  Any shape: 3x3 stride-1 convolutions with Cin 32 or 64, Cout a
+ * alike).  Any shape: 3x3 stride-1 convolutions with Cin 32, 64 or 128, Cout a
  * multiple of 32 and Wo <= 64 take the row-block kernel; Cin a multiple of
  * 32 with Cout a multiple of 64 the implicit-GEMM kernel; everything else a
  * direct kernel.

@@ -230,6 +230,9 @@ CONV_SHAPES = [
     (1, 4, 64, 64, 64, 3, 3, 1, 0),   # row-pair, widest row, no padding
     (1, 7, 56, 64, 32, 3, 3, 1, 1),   # row-block 4 rows x 32 channels (Cout 32), last block half outside
     (2, 5, 30, 32, 96, 3, 3, 1, 1),   # row-block 4 x 32, three channel blocks, Cin 32
+    (2, 7, 28, 128, 128, 3, 3, 1, 1),  # row-block 2 x 64 at Cin 128 (108 KiB of LDS), odd Ho
+    (1, 6, 60, 128, 96, 3, 3, 1, 2),  # row-block 4 x 32 at Cin 128, pad 2
+    (1, 5, 9, 96, 64, 3, 3, 1, 1),    # Cin 96: implicit-GEMM kernel
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # fallback kernel (channels not multiples of 32/64)
     (2, 6, 7, 3, 5, 3, 3, 2, 0),      # fallback kernel
 ]
@@ -256,6 +259,7 @@ def test_conv2d_i8(ctx, shape):
 @pytest.mark.parametrize("shape", [
     (1, 6, 56, 64, 64, 3, 3, 1, 1),   # row-block 2 rows x 64 channels
     (1, 5, 20, 32, 96, 3, 3, 1, 1),   # row-block 4 rows x 32 channels
+    (1, 4, 24, 128, 64, 3, 3, 1, 1),  # row-block at Cin 128
     (1, 8, 8, 64, 64, 3, 3, 2, 1),    # implicit-GEMM kernel
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # direct kernel
 ])
