@@ -836,6 +836,79 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64(const int8_t* __restrict__
   }
 }
 
+// The 64x64 kernel for K % 64 == 0 and 16-byte aligned operands (a ragged M
+// or N): every load is a full vector from a clamped, always valid address,
+// zeroed when written to LDS if outside the matrix, and the next k-tile's
+// loads are issued before this k-tile's LDS reads and MFMAs, so their
+// latency overlaps the MFMAs (a load under a condition, or zeroed in place,
+// would be waited for on the spot).
+template <bool B_NT>
+__global__ __launch_bounds__(256) void gemm_i8_tile64p(const int8_t* __restrict__ A,
+                                                       const int8_t* __restrict__ B,
+                                                       int8_t* __restrict__ Y, int32_t* __restrict__ C,
+                                                       int M, int N, int K, int lda, int ldb, int ldy,
+                                                       int ldc, int shift, int relu) {
+  __shared__ __attribute__((aligned(16))) int8_t as[64 * 64];
+  __shared__ __attribute__((aligned(16))) int8_t bs[64 * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fr = lane & 31, fh = lane >> 5;
+
+  // A (and NT B): thread -> row tid/4, 16-byte chunk tid%4
+  const int row = tid >> 2, ch = tid & 3;
+  const bool a_in = m0 + row < M;
+  const int8_t* const a_p = A + (size_t)min(m0 + row, M - 1) * lda + ch * 16;
+  // NT B: row n0 + row; NN B: column n0 + tid%64, k-chunk tid/64 (16 byte loads down the column)
+  const int bcol = tid & 63, bch = tid >> 6;
+  const bool b_in = B_NT ? n0 + row < N : n0 + bcol < N;
+  const int8_t* const b_p = B_NT ? B + (size_t)min(n0 + row, N - 1) * ldb + ch * 16
+                                 : B + (size_t)(bch * 16) * ldb + min(n0 + bcol, N - 1);
+
+  auto load = [&](int k0, v4i& va, v4i& vb) {
+    va = *reinterpret_cast<const v4i*>(a_p + k0);
+    if constexpr (B_NT) {
+      vb = *reinterpret_cast<const v4i*>(b_p + k0);
+    } else {
+      int8_t tmp[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) tmp[t] = b_p[(size_t)(k0 + t) * ldb];
+      __builtin_memcpy(&vb, tmp, 16);
+    }
+  };
+
+  v16i acc = v16i{0};
+  v4i va, vb;
+  load(0, va, vb);
+  for (int k0 = 0; k0 < K; k0 += 64) {
+    *reinterpret_cast<v4i*>(as + lds_off(row, ch)) = a_in ? va : v4i{0};
+    if constexpr (B_NT)
+      *reinterpret_cast<v4i*>(bs + lds_off(row, ch)) = b_in ? vb : v4i{0};
+    else
+      *reinterpret_cast<v4i*>(bs + lds_off(bcol, bch)) = b_in ? vb : v4i{0};
+    __syncthreads();
+    if (k0 + 64 < K) load(k0 + 64, va, vb);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const v4i af = *reinterpret_cast<const v4i*>(as + lds_off(wm * 32 + fr, 2 * ks + fh));
+      const v4i bf = *reinterpret_cast<const v4i*>(bs + lds_off(wn * 32 + fr, 2 * ks + fh));
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af, acc, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  const int m = m0 + wm * 32 + fr;
+  if (m >= M) return;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int n = n0 + wn * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
+    if (n < N) {
+      if (C) C[(size_t)m * ldc + n] = acc[e];
+      if (Y) Y[(size_t)m * ldy + n] = (int8_t)requant1(acc[e], shift, relu);
+    }
+  }
+}
+
 template <int BM, int BN, bool B_NT>
 void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
                  int lda, int ldb, int ldy, int ldc, int shift, int relu) {
@@ -971,6 +1044,17 @@ int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, 
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64), block(256);
   if (grid.y > 65535) return fail(ctx, MIAIE_EINVAL, "gemm_i8: M too large for the 64x64 fallback");
+  // vector loads need K % 64 == 0 and 16-byte aligned A (and NT B) rows
+  const bool vec = K % BK == 0 && aligned(A, 16) && lda % 16 == 0 && (!b_nt || (aligned(B, 16) && ldb % 16 == 0));
+  if (vec) {
+    if (b_nt)
+      hipLaunchKernelGGL(gemm_i8_tile64p<true>, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy,
+                         ldc, shift, relu);
+    else
+      hipLaunchKernelGGL(gemm_i8_tile64p<false>, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy,
+                         ldc, shift, relu);
+    return check_launch(ctx, "gemm_i8_tile64p");
+  }
   if (b_nt)
     hipLaunchKernelGGL(gemm_i8_tile64<true>, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb,
                        ldy, ldc, shift, relu);

@@ -159,3 +159,53 @@ def test_strided_operands(ctx, M, N, K, lda, ldb, ldc, layout):
             b.free()
     finally:
         ctx.plan_set_cus(prev)
+
+
+# Ragged M / N with K % 64 == 0 and 16-byte aligned A rows take the
+# prefetching 64x64 kernel (vector loads from clamped addresses, zeroed
+# outside the matrix); bit-exact in every output mode and both B layouts,
+# including products smaller than one tile and row pitches above the extent.
+@pytest.mark.parametrize("M,N,K,layout,lda_pad", [
+    (1000, 1008, 256, mi.B_NN, 0),
+    (300, 4000, 128, mi.B_NN, 0),
+    (129, 77, 64, mi.B_NN, 0),    # N not a multiple of 16: byte gathers down B's columns
+    (33, 250, 192, mi.B_NT, 0),
+    (2000, 100, 128, mi.B_NT, 0),
+    (1, 1, 64, mi.B_NN, 0),
+    (70, 130, 128, mi.B_NN, 16),  # lda = K + 16
+    (70, 130, 128, mi.B_NT, 32),  # lda = K + 32, ldb = K + 32
+])
+def test_ragged_fallback_matches_the_oracle(ctx, M, N, K, layout, lda_pad):
+    plan = ctx.plan_gemm_i8(M, N, K)
+    print(f"[case] ragged gemm {M}x{N}x{K} layout {layout} pad {lda_pad} plan {plan}", flush=True)
+    assert plan["kernel"] == mi.KERNEL_TILE64
+    rng = np.random.default_rng(M * 7 + N * 3 + K + layout + lda_pad)
+    lda = K + lda_pad
+    Ab = rng.integers(-128, 128, size=(M, lda), dtype=np.int8)
+    if layout == mi.B_NT:
+        ldb = K + lda_pad
+        Bb = rng.integers(-128, 128, size=(N, ldb), dtype=np.int8)
+        B = np.ascontiguousarray(Bb[:, :K])
+    else:
+        ldb = N
+        Bb = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+        B = Bb
+    A = np.ascontiguousarray(Ab[:, :K])
+    C = oracle.gemm_i8(A, B, b_nt=layout == mi.B_NT)
+    dA, dB = ctx.upload(Ab), ctx.upload(Bb)
+    dC = ctx.empty((M, N), np.int32)
+    ctx.gemm_i8_i32(dA, dB, dC, M, N, K, lda=lda, ldb=ldb, ldc=N, b_layout=layout)
+    ctx.wait(60_000)
+    assert np.array_equal(ctx.download(dC), C)
+    if lda_pad == 0:  # the requantizing entry takes dense operands
+        dY, dY2, dC2 = ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int32)
+        ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, layout)
+        ctx.gemm_i8_rq(dA, dB, dY2, M, N, K, 5, True, dC2, layout)
+        ctx.wait(60_000)
+        assert np.array_equal(ctx.download(dY), oracle.requant(C, 10))
+        assert np.array_equal(ctx.download(dY2), oracle.requant(C, 5, relu=True))
+        assert np.array_equal(ctx.download(dC2), C)
+        for b in (dY, dY2, dC2):
+            b.free()
+    for b in (dA, dB, dC):
+        b.free()
