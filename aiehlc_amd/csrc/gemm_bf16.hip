@@ -513,6 +513,57 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restri
   }
 }
 
+// The 64x64 kernel for K % 32 == 0 and a 16-byte aligned A (a ragged M or
+// N): A rows are loaded as full vectors and B columns gathered from clamped,
+// always valid addresses, zeroed when written to LDS if outside the matrix,
+// and the next k-tile's loads are issued before this k-tile's LDS reads and
+// MFMAs, so their latency overlaps the MFMAs.
+__global__ __launch_bounds__(256) void gemm_bf16_tile64p(const uint16_t* __restrict__ A,
+                                                         const uint16_t* __restrict__ B,
+                                                         float* __restrict__ C, int M, int N, int K) {
+  __shared__ __attribute__((aligned(16))) int8_t as[64 * 64];
+  __shared__ __attribute__((aligned(16))) int8_t bs[64 * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fr = lane & 31, fh = lane >> 5;
+  // A: thread -> row tid/4, 8-element chunk tid%4; B: column tid%64, k-chunk tid/64
+  const int row = tid >> 2, ch = tid & 3, col = tid & 63, bch = tid >> 6;
+  const bool a_in = m0 + row < M, b_in = n0 + col < N;
+  const uint16_t* const a_p = A + (size_t)min(m0 + row, M - 1) * K + ch * 8;
+  const uint16_t* const b_p = B + (size_t)(bch * 8) * N + min(n0 + col, N - 1);
+  auto load = [&](int k0, v4i& va, v4i& vb) {
+    va = *reinterpret_cast<const v4i*>(a_p + k0);
+    uint16_t tmp[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) tmp[t] = b_p[(size_t)(k0 + t) * N];
+    __builtin_memcpy(&vb, tmp, 16);
+  };
+  v16f acc = v16f{0.f};
+  v4i va, vb;
+  load(0, va, vb);
+  for (int k0 = 0; k0 < K; k0 += 32) {
+    *reinterpret_cast<v4i*>(as + lds_off(row, ch)) = a_in ? va : v4i{0};
+    *reinterpret_cast<v4i*>(bs + lds_off(col, bch)) = b_in ? vb : v4i{0};
+    __syncthreads();
+    if (k0 + 32 < K) load(k0 + 32, va, vb);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const v4i af = *reinterpret_cast<const v4i*>(as + lds_off(wm * 32 + fr, 2 * ks + fh));
+      const v4i bf = *reinterpret_cast<const v4i*>(bs + lds_off(wn * 32 + fr, 2 * ks + fh));
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(bf), as_bf(af), acc, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  const int m = m0 + wm * 32 + fr;
+  if (m >= M) return;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int n = n0 + wn * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
+    if (n < N) C[(size_t)m * N + n] = acc[e];
+  }
+}
+
 }  // namespace
 
 namespace miaie {
@@ -532,6 +583,10 @@ int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64);
   if (grid.y > 65535) return fail(ctx, MIAIE_EINVAL, "gemm_bf16: M too large for the 64x64 fallback");
+  if (K % 32 == 0 && aligned(A, 16)) {
+    hipLaunchKernelGGL(gemm_bf16_tile64p, grid, dim3(256), 0, ctx->stream, A, B, C, M, N, K);
+    return check_launch(ctx, "gemm_bf16_tile64p");
+  }
   hipLaunchKernelGGL(gemm_bf16_tile64, grid, dim3(256), 0, ctx->stream, A, B, C, M, N, K);
   return check_launch(ctx, "gemm_bf16_tile64");
 }

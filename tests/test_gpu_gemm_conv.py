@@ -137,7 +137,8 @@ def test_gemm_i8_rq_4096_config(ctx):
     assert np.array_equal(Ch2.astype(np.int64), 2 * Ch.astype(np.int64))
 
 
-@pytest.mark.parametrize("shape", [(1, 1, 1), (64, 64, 64), (37, 70, 45), (256, 256, 32), (512, 256, 512)])
+@pytest.mark.parametrize("shape", [(1, 1, 1), (64, 64, 64), (37, 70, 45), (256, 256, 32), (512, 256, 512),
+                                   (300, 1000, 256), (129, 77, 64), (1000, 40, 96)])  # last three: prefetching 64x64
 def test_gemm_bf16(ctx, shape):
     M, N, K = shape
     _say("gemm_bf16", shape)
