@@ -9,6 +9,8 @@
 // the row-major B operand is 16-bit-transposed in registers on its way to LDS.
 //   gemm_bf16_pair     256x256, K % 64 == 0: A staged two k-tiles at a time.
 //   gemm_bf16_tile256  256x256x32, 4 waves x (4x4 MFMA 32x32x16), four LDS stages.
+//   gemm_bf16_tile64p  64x64x32 fallback for K % 32 == 0 and an aligned A:
+//                      vector A loads, next k-tile prefetched into registers.
 //   gemm_bf16_tile64   64x64x32 bounds-checked fallback.
 // Both 256x256 kernels write C through store_tile_f32 (whole-row stores).
 #include <type_traits>

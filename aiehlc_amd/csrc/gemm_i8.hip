@@ -15,6 +15,9 @@
 //                   XCD-aware tile order.  M % BM == N % BN == K % 64 == 0.
 //   gemm_i8_pipe2   the same with A staged two k-tiles at a time, so A copies
 //                   move whole cache lines (256-row tiles, K % 128 == 0).
+//   gemm_i8_tile64p 64x64x64 tile for K % 64 == 0 and 16-byte aligned rows
+//                   (a ragged M or N): clamped vector loads, next k-tile
+//                   prefetched into registers.
 //   gemm_i8_tile64  64x64x64 tile, bounds-checked, any shape / stride.
 // The requantize epilogue (round, shift, saturate, optional ReLU) is fused
 // into all of them.
