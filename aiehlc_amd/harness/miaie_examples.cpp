@@ -210,7 +210,7 @@ int run_conv(miaie::Context& ctx) {
   dX.move_in(X);
   dW.move_in(W);
   dS.move_in(sh);
-  ctx.check(miaie_conv2d_i8_nhwc(ctx.get(), dX.data(), dW.data(), dS.data(), dY.data(), Nb, H, Wd, C, Co, 3, 3, 1, 1));
+  miaie::conv2d_i8(dX, dW, dS, dY, miaie::ConvShape{Nb, H, Wd, C, Co}, ctx);
   if (!ctx.wait(kDeadlineMs)) return 2;
   const std::vector<int8_t> Y = dY.move_out();
   int mismatches = 0;
@@ -239,7 +239,7 @@ int run_mlp(miaie::Context& ctx, int M, int K, int F, int Nout) {
   dX.move_in(X);
   d1.move_in(W1);
   d2.move_in(W2);
-  ctx.check(miaie_mlp_i8(ctx.get(), dX.data(), d1.data(), d2.data(), dH.data(), dY.data(), M, K, F, Nout, 11, 12));
+  miaie::mlp_i8(dX, d1, d2, dH, dY, M, K, F, Nout, 11, 12, ctx);
   if (!ctx.wait(kDeadlineMs)) return 2;
   const std::vector<int8_t> Y = dY.move_out();
   int mismatches = 0;

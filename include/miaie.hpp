@@ -179,6 +179,53 @@ void gemm_bf16(const uint16_t* A, const uint16_t* B, float* C, Context& ctx = Co
   ctx.check(miaie_gemm_bf16_f32(ctx.get(), A, B, C, M, N, K));
 }
 
+// ---------------------------------------------------------------- runtime-shape operators
+// The typed entry points with shapes known at run time, on device buffers.
+// Asynchronous on the context's stream, like the launch templates above.
+
+// Y = rq_shift(A . B) (NN or NT B, layout MIAIE_B_NN / MIAIE_B_NT); C_dbg
+// (nullable) receives the int32 accumulators.
+inline void gemm_i8_rq(const Buffer<int8_t>& A, const Buffer<int8_t>& B, Buffer<int8_t>& Y, int M, int N, int K,
+                       int shift, bool relu = false, Buffer<int32_t>* C_dbg = nullptr, int b_layout = MIAIE_B_NN,
+                       Context& ctx = Context::current()) {
+  ctx.check(miaie_gemm_i8_rq(ctx.get(), A.data(), B.data(), Y.data(), M, N, K, shift, relu ? 1 : 0,
+                             C_dbg ? C_dbg->data() : nullptr, b_layout));
+}
+
+// C = A . B in int32, with row pitches (elements) lda / ldb / ldc.
+inline void gemm_i8_i32(const Buffer<int8_t>& A, const Buffer<int8_t>& B, Buffer<int32_t>& C, int M, int N, int K,
+                        int lda, int ldb, int ldc, int b_layout = MIAIE_B_NN, Context& ctx = Context::current()) {
+  ctx.check(miaie_gemm_i8_i32(ctx.get(), A.data(), B.data(), C.data(), M, N, K, lda, ldb, ldc, b_layout));
+}
+
+// C = A . B, bf16 in (raw uint16 bits), fp32 accumulate and out, NN.
+inline void gemm_bf16(const Buffer<uint16_t>& A, const Buffer<uint16_t>& B, Buffer<float>& C, int M, int N, int K,
+                      Context& ctx = Context::current()) {
+  ctx.check(miaie_gemm_bf16_f32(ctx.get(), A.data(), B.data(), C.data(), M, N, K));
+}
+
+// Shape of an NHWC x OHWI convolution.
+struct ConvShape {
+  int N, H, W, Cin, Cout, R = 3, S = 3, stride = 1, pad = 1;
+  int Ho() const { return (H + 2 * pad - R) / stride + 1; }
+  int Wo() const { return (W + 2 * pad - S) / stride + 1; }
+};
+
+// Y[N][Ho][Wo][Cout] = per-channel rq(conv(X, Wt)), shifts[c] in [0, 31].
+inline void conv2d_i8(const Buffer<int8_t>& X, const Buffer<int8_t>& Wt, const Buffer<uint8_t>& shifts,
+                      Buffer<int8_t>& Y, const ConvShape& c, Context& ctx = Context::current()) {
+  ctx.check(miaie_conv2d_i8_nhwc(ctx.get(), X.data(), Wt.data(), shifts.data(), Y.data(), c.N, c.H, c.W, c.Cin,
+                                 c.Cout, c.R, c.S, c.stride, c.pad));
+}
+
+// H = relu(rq_s1(X . W1)), Y = rq_s2(H . W2); H is caller-provided device
+// scratch of M x F.
+inline void mlp_i8(const Buffer<int8_t>& X, const Buffer<int8_t>& W1, const Buffer<int8_t>& W2, Buffer<int8_t>& H,
+                   Buffer<int8_t>& Y, int M, int K, int F, int Nout, int s1, int s2,
+                   Context& ctx = Context::current()) {
+  ctx.check(miaie_mlp_i8(ctx.get(), X.data(), W1.data(), W2.data(), H.data(), Y.data(), M, K, F, Nout, s1, s2));
+}
+
 }  // namespace miaie
 
 #endif  // MIAIE_HPP
