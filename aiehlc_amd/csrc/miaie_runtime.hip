@@ -283,8 +283,12 @@ extern "C" int miaie_wait(miaie_ctx* ctx, int timeout_ms) {
     double ms = (t1.tv_sec - t0.tv_sec) * 1e3 + (t1.tv_nsec - t0.tv_nsec) * 1e-6;
     if (ms >= timeout_ms)
       return fail(ctx, MIAIE_ETIMEDOUT, "miaie_wait: stream not drained after %d ms", timeout_ms);
-    timespec nap = {0, 20000};  // 20 us
-    nanosleep(&nap, nullptr);
+    // poll without sleeping for the first 0.2 ms (a short kernel finishes
+    // within a few microseconds and a 20 us nap would dominate), then nap
+    if (ms >= 0.2) {
+      timespec nap = {0, 20000};  // 20 us
+      nanosleep(&nap, nullptr);
+    }
   }
 }
 
