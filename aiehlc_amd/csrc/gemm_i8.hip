@@ -15,9 +15,9 @@
 //                   XCD-aware tile order.  M % BM == N % BN == K % 64 == 0.
 //   gemm_i8_pipe2   the same with A staged two k-tiles at a time, so A copies
 //                   move whole cache lines (256-row tiles, K % 128 == 0).
-//   gemm_i8_tile64p 64x64x64 tile for K % 64 == 0 and 16-byte aligned rows
-//                   (a ragged M or N): clamped vector loads, next k-tile
-//                   prefetched into registers.
+//   gemm_i8_tile64p 64x64x64 tile for K % 16 == 0 and 16-byte aligned rows:
+//                   clamped vector loads, next k-tile prefetched into
+//                   registers.
 //   gemm_i8_tile64  64x64x64 tile, bounds-checked, any shape / stride.
 // The requantize epilogue (round, shift, saturate, optional ReLU) is fused
 // into all of them.
@@ -839,8 +839,8 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64(const int8_t* __restrict__
   }
 }
 
-// The 64x64 kernel for K % 64 == 0 and 16-byte aligned operands (a ragged M
-// or N): every load is a full vector from a clamped, always valid address,
+// The 64x64 kernel for K % 16 == 0 and 16-byte aligned operands (a ragged M,
+// N or K): every load is a full vector from a clamped, always valid address,
 // zeroed when written to LDS if outside the matrix, and the next k-tile's
 // loads are issued before this k-tile's LDS reads and MFMAs, so their
 // latency overlaps the MFMAs (a load under a condition, or zeroed in place,
@@ -858,24 +858,27 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64p(const int8_t* __restrict_
   const int wm = wave >> 1, wn = wave & 1;
   const int fr = lane & 31, fh = lane >> 5;
 
-  // A (and NT B): thread -> row tid/4, 16-byte chunk tid%4
+  // A (and NT B): thread -> row tid/4, 16-byte chunk tid%4.  K % 16 == 0, so
+  // a chunk lies wholly inside or wholly past K; one past K loads the last
+  // chunk of its row instead and is zeroed like a row outside the matrix.
   const int row = tid >> 2, ch = tid & 3;
   const bool a_in = m0 + row < M;
-  const int8_t* const a_p = A + (size_t)min(m0 + row, M - 1) * lda + ch * 16;
+  const int8_t* const a_p = A + (size_t)min(m0 + row, M - 1) * lda;
   // NT B: row n0 + row; NN B: column n0 + tid%64, k-chunk tid/64 (16 byte loads down the column)
   const int bcol = tid & 63, bch = tid >> 6;
   const bool b_in = B_NT ? n0 + row < N : n0 + bcol < N;
-  const int8_t* const b_p = B_NT ? B + (size_t)min(n0 + row, N - 1) * ldb + ch * 16
-                                 : B + (size_t)(bch * 16) * ldb + min(n0 + bcol, N - 1);
+  const int8_t* const b_p = B_NT ? B + (size_t)min(n0 + row, N - 1) * ldb : B + min(n0 + bcol, N - 1);
+  const int bk = B_NT ? ch : bch;  // this thread's k-chunk of B
 
   auto load = [&](int k0, v4i& va, v4i& vb) {
-    va = *reinterpret_cast<const v4i*>(a_p + k0);
+    va = *reinterpret_cast<const v4i*>(a_p + min(k0 + 16 * ch, K - 16));
     if constexpr (B_NT) {
-      vb = *reinterpret_cast<const v4i*>(b_p + k0);
+      vb = *reinterpret_cast<const v4i*>(b_p + min(k0 + 16 * ch, K - 16));
     } else {
+      const int8_t* const p = b_p + (size_t)min(k0 + 16 * bch, K - 16) * ldb;
       int8_t tmp[16];
 #pragma unroll
-      for (int t = 0; t < 16; ++t) tmp[t] = b_p[(size_t)(k0 + t) * ldb];
+      for (int t = 0; t < 16; ++t) tmp[t] = p[(size_t)t * ldb];
       __builtin_memcpy(&vb, tmp, 16);
     }
   };
@@ -884,11 +887,11 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64p(const int8_t* __restrict_
   v4i va, vb;
   load(0, va, vb);
   for (int k0 = 0; k0 < K; k0 += 64) {
-    *reinterpret_cast<v4i*>(as + lds_off(row, ch)) = a_in ? va : v4i{0};
+    *reinterpret_cast<v4i*>(as + lds_off(row, ch)) = a_in && k0 + 16 * ch < K ? va : v4i{0};
     if constexpr (B_NT)
-      *reinterpret_cast<v4i*>(bs + lds_off(row, ch)) = b_in ? vb : v4i{0};
+      *reinterpret_cast<v4i*>(bs + lds_off(row, ch)) = b_in && k0 + 16 * bk < K ? vb : v4i{0};
     else
-      *reinterpret_cast<v4i*>(bs + lds_off(bcol, bch)) = b_in ? vb : v4i{0};
+      *reinterpret_cast<v4i*>(bs + lds_off(bcol, bch)) = b_in && k0 + 16 * bk < K ? vb : v4i{0};
     __syncthreads();
     if (k0 + 64 < K) load(k0 + 64, va, vb);
 #pragma unroll
@@ -1047,8 +1050,8 @@ int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, 
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64), block(256);
   if (grid.y > 65535) return fail(ctx, MIAIE_EINVAL, "gemm_i8: M too large for the 64x64 fallback");
-  // vector loads need K % 64 == 0 and 16-byte aligned A (and NT B) rows
-  const bool vec = K % BK == 0 && aligned(A, 16) && lda % 16 == 0 && (!b_nt || (aligned(B, 16) && ldb % 16 == 0));
+  // vector loads need K % 16 == 0 and 16-byte aligned A (and NT B) rows
+  const bool vec = K % 16 == 0 && aligned(A, 16) && lda % 16 == 0 && (!b_nt || (aligned(B, 16) && ldb % 16 == 0));
   if (vec) {
     if (b_nt)
       hipLaunchKernelGGL(gemm_i8_tile64p<true>, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy,

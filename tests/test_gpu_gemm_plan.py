@@ -161,8 +161,8 @@ def test_strided_operands(ctx, M, N, K, lda, ldb, ldc, layout):
         ctx.plan_set_cus(prev)
 
 
-# Ragged M / N with K % 64 == 0 and 16-byte aligned A rows take the
-# prefetching 64x64 kernel (vector loads from clamped addresses, zeroed
+# Ragged M / N (or K % 64 != 0) with K % 16 == 0 and 16-byte aligned A rows
+# take the prefetching 64x64 kernel (vector loads from clamped addresses, zeroed
 # outside the matrix); bit-exact in every output mode and both B layouts,
 # including products smaller than one tile and row pitches above the extent.
 @pytest.mark.parametrize("M,N,K,layout,lda_pad", [
@@ -174,6 +174,10 @@ def test_strided_operands(ctx, M, N, K, lda, ldb, ldc, layout):
     (1, 1, 64, mi.B_NN, 0),
     (70, 130, 128, mi.B_NN, 16),  # lda = K + 16
     (70, 130, 128, mi.B_NT, 32),  # lda = K + 32, ldb = K + 32
+    (100, 130, 80, mi.B_NN, 0),   # K % 64 == 16: the last k-tile is one chunk deep
+    (65, 33, 48, mi.B_NT, 0),     # K % 64 == 48, one k-tile
+    (300, 272, 1008, mi.B_NN, 0),
+    (64, 64, 16, mi.B_NT, 16),    # K = 16, lda = ldb = 32
 ])
 def test_ragged_fallback_matches_the_oracle(ctx, M, N, K, layout, lda_pad):
     plan = ctx.plan_gemm_i8(M, N, K)
