@@ -9,7 +9,7 @@
 // the row-major B operand is 16-bit-transposed in registers on its way to LDS.
 //   gemm_bf16_pair     256x256, K % 64 == 0: A staged two k-tiles at a time.
 //   gemm_bf16_tile256  256x256x32, 4 waves x (4x4 MFMA 32x32x16), four LDS stages.
-//   gemm_bf16_tile64p  64x64x32 fallback for K % 32 == 0 and an aligned A:
+//   gemm_bf16_tile64p  64x64x32 fallback for K % 8 == 0 and an aligned A:
 //                      vector A loads, next k-tile prefetched into registers.
 //   gemm_bf16_tile64   64x64x32 bounds-checked fallback.
 // Both 256x256 kernels write C through store_tile_f32 (whole-row stores).
@@ -515,8 +515,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restri
   }
 }
 
-// The 64x64 kernel for K % 32 == 0 and a 16-byte aligned A (a ragged M or
-// N): A rows are loaded as full vectors and B columns gathered from clamped,
+// The 64x64 kernel for K % 8 == 0 and a 16-byte aligned A (a ragged M, N
+// or K): A rows are loaded as full vectors and B columns gathered from clamped,
 // always valid addresses, zeroed when written to LDS if outside the matrix,
 // and the next k-tile's loads are issued before this k-tile's LDS reads and
 // MFMAs, so their latency overlaps the MFMAs.
@@ -531,22 +531,25 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64p(const uint16_t* __restr
   const int fr = lane & 31, fh = lane >> 5;
   // A: thread -> row tid/4, 8-element chunk tid%4; B: column tid%64, k-chunk tid/64
   const int row = tid >> 2, ch = tid & 3, col = tid & 63, bch = tid >> 6;
+  // K % 8 == 0: an 8-element k-chunk lies wholly inside or wholly past K; one
+  // past K loads the row's last chunk instead and is zeroed
   const bool a_in = m0 + row < M, b_in = n0 + col < N;
-  const uint16_t* const a_p = A + (size_t)min(m0 + row, M - 1) * K + ch * 8;
-  const uint16_t* const b_p = B + (size_t)(bch * 8) * N + min(n0 + col, N - 1);
+  const uint16_t* const a_p = A + (size_t)min(m0 + row, M - 1) * K;
+  const uint16_t* const b_p = B + min(n0 + col, N - 1);
   auto load = [&](int k0, v4i& va, v4i& vb) {
-    va = *reinterpret_cast<const v4i*>(a_p + k0);
+    va = *reinterpret_cast<const v4i*>(a_p + min(k0 + 8 * ch, K - 8));
+    const uint16_t* const p = b_p + (size_t)min(k0 + 8 * bch, K - 8) * N;
     uint16_t tmp[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) tmp[t] = b_p[(size_t)(k0 + t) * N];
+    for (int t = 0; t < 8; ++t) tmp[t] = p[(size_t)t * N];
     __builtin_memcpy(&vb, tmp, 16);
   };
   v16f acc = v16f{0.f};
   v4i va, vb;
   load(0, va, vb);
   for (int k0 = 0; k0 < K; k0 += 32) {
-    *reinterpret_cast<v4i*>(as + lds_off(row, ch)) = a_in ? va : v4i{0};
-    *reinterpret_cast<v4i*>(bs + lds_off(col, bch)) = b_in ? vb : v4i{0};
+    *reinterpret_cast<v4i*>(as + lds_off(row, ch)) = a_in && k0 + 8 * ch < K ? va : v4i{0};
+    *reinterpret_cast<v4i*>(bs + lds_off(col, bch)) = b_in && k0 + 8 * bch < K ? vb : v4i{0};
     __syncthreads();
     if (k0 + 32 < K) load(k0 + 32, va, vb);
 #pragma unroll
@@ -585,7 +588,7 @@ int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64);
   if (grid.y > 65535) return fail(ctx, MIAIE_EINVAL, "gemm_bf16: M too large for the 64x64 fallback");
-  if (K % 32 == 0 && aligned(A, 16)) {
+  if (K % 8 == 0 && aligned(A, 16)) {
     hipLaunchKernelGGL(gemm_bf16_tile64p, grid, dim3(256), 0, ctx->stream, A, B, C, M, N, K);
     return check_launch(ctx, "gemm_bf16_tile64p");
   }

@@ -138,7 +138,8 @@ def test_gemm_i8_rq_4096_config(ctx):
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 1), (64, 64, 64), (37, 70, 45), (256, 256, 32), (512, 256, 512),
-                                   (300, 1000, 256), (129, 77, 64), (1000, 40, 96)])  # last three: prefetching 64x64
+                                   (300, 1000, 256), (129, 77, 64), (1000, 40, 96),  # prefetching 64x64
+                                   (100, 130, 40), (33, 65, 8), (70, 70, 1000)])     # ... with K % 32 != 0
 def test_gemm_bf16(ctx, shape):
     M, N, K = shape
     _say("gemm_bf16", shape)
