@@ -77,6 +77,7 @@ _SIGS = {
     "miaie_fill_i8": (_i, [_p, _p, _sz, _u64]),
     "miaie_plan_gemm_i8": (_i, [_p, _i, _i, _i, _p]),
     "miaie_plan_set_cus": (_i, [_p, _i, C.POINTER(_i)]),
+    "miaie_plan_conv2d_i8": (_i, [_i] * 9 + [C.POINTER(_i)]),
     "miaie_graph_begin": (_i, [_p]),
     "miaie_graph_end": (_i, [_p, C.POINTER(_p)]),
     "miaie_graph_launch": (_i, [_p, _p]),
@@ -108,6 +109,19 @@ def header_functions(path: str = HEADER_PATH) -> list[str]:
     """Names of every MIAIE_API function declared in include/miaie.h."""
     text = open(path).read()
     return re.findall(r"MIAIE_API\s+[\w\s\*]+?\b(miaie_\w+)\s*\(", text)
+
+
+CONV_KERNELS = {0: "rows", 1: "igemm", 2: "direct"}  # MIAIE_CONV_*
+
+
+def plan_conv2d_i8(N, H, W, Cin, Cout, R=3, S=3, stride=1, pad=1) -> str:
+    """Which conv kernel miaie_conv2d_i8_nhwc runs for this shape (16-byte
+    aligned buffers).  A host function: needs no device."""
+    k = _i(-1)
+    rc = load_library().miaie_plan_conv2d_i8(N, H, W, Cin, Cout, R, S, stride, pad, C.byref(k))
+    if rc != MIAIE_OK:
+        raise MiaieError(rc, load_library().miaie_last_error_string(None).decode())
+    return CONV_KERNELS[k.value]
 
 
 class DeviceBuffer:

@@ -70,6 +70,32 @@ extern "C" int miaie_gemm_bf16_f32(miaie_ctx* ctx, const uint16_t* A, const uint
   return launch_gemm_bf16(ctx, A, B, C, M, N, K);
 }
 
+namespace {
+
+int check_conv_shape(miaie_ctx* ctx, const char* fn, int N, int H, int W_, int Cin, int Cout, int R, int S,
+                     int stride, int pad) {
+  if (N < 1 || H < 1 || W_ < 1 || Cin < 1 || Cout < 1 || R < 1 || S < 1 || stride < 1 || pad < 0)
+    return fail(ctx, MIAIE_EINVAL, "%s: invalid shape N=%d H=%d W=%d Cin=%d Cout=%d R=%d S=%d stride=%d pad=%d",
+                fn, N, H, W_, Cin, Cout, R, S, stride, pad);
+  if (H + 2 * pad < R || W_ + 2 * pad < S)
+    return fail(ctx, MIAIE_EINVAL, "%s: filter %dx%d larger than the padded input %dx%d", fn, R, S, H + 2 * pad,
+                W_ + 2 * pad);
+  if ((size_t)R * S * Cin > (1u << 30) || (size_t)N * H * W_ * Cin > ((size_t)1 << 40))
+    return fail(ctx, MIAIE_EINVAL, "%s: problem too large", fn);
+  return MIAIE_OK;
+}
+
+}  // namespace
+
+extern "C" int miaie_plan_conv2d_i8(int N, int H, int W_, int Cin, int Cout, int R, int S, int stride, int pad,
+                                    int* kernel) {
+  if (!kernel) return fail(nullptr, MIAIE_EINVAL, "%s: kernel is NULL", __func__);
+  int rc = check_conv_shape(nullptr, __func__, N, H, W_, Cin, Cout, R, S, stride, pad);
+  if (rc) return rc;
+  *kernel = conv2d_kernel_for(N, H, W_, Cin, Cout, R, S, stride, pad, true, true);
+  return MIAIE_OK;
+}
+
 extern "C" int miaie_conv2d_i8_nhwc(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts,
                                     int8_t* Y, int N, int H, int W_, int Cin, int Cout, int R, int S, int stride,
                                     int pad) {
@@ -79,14 +105,7 @@ extern "C" int miaie_conv2d_i8_nhwc(miaie_ctx* ctx, const int8_t* X, const int8_
   MIAIE_CHECK_NOT_NULL(ctx, W);
   MIAIE_CHECK_NOT_NULL(ctx, shifts);
   MIAIE_CHECK_NOT_NULL(ctx, Y);
-  if (N < 1 || H < 1 || W_ < 1 || Cin < 1 || Cout < 1 || R < 1 || S < 1 || stride < 1 || pad < 0)
-    return fail(ctx, MIAIE_EINVAL, "%s: invalid shape N=%d H=%d W=%d Cin=%d Cout=%d R=%d S=%d stride=%d pad=%d",
-                __func__, N, H, W_, Cin, Cout, R, S, stride, pad);
-  if (H + 2 * pad < R || W_ + 2 * pad < S)
-    return fail(ctx, MIAIE_EINVAL, "%s: filter %dx%d larger than the padded input %dx%d", __func__, R, S,
-                H + 2 * pad, W_ + 2 * pad);
-  if ((size_t)R * S * Cin > (1u << 30) || (size_t)N * H * W_ * Cin > ((size_t)1 << 40))
-    return fail(ctx, MIAIE_EINVAL, "%s: problem too large", __func__);
+  if ((rc = check_conv_shape(ctx, __func__, N, H, W_, Cin, Cout, R, S, stride, pad))) return rc;
   return launch_conv2d_i8(ctx, X, W, shifts, Y, N, H, W_, Cin, Cout, R, S, stride, pad);
 }
 

@@ -378,24 +378,38 @@ static int launch_rows(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const u
   return check_launch(ctx, "conv2d_i8_rows");
 }
 
+int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad, bool aligned16,
+                      bool shifts_aligned4) {
+  const int Ho = (H + 2 * pad - R) / stride + 1;
+  const int Wo = (Wd + 2 * pad - S) / stride + 1;
+  const size_t P = (size_t)N * Ho * Wo;
+  // Row-block kernel (3x3, stride 1, Cin 32, 64 or 128, Wo <= 64).  Its
+  // offsets are 32-bit: X, Y and W (co0 * R*S*Cin) must each stay below
+  // 2^31 bytes, and the channel blocks (>= 32 channels each) fit grid.y.
+  const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64 || Cin == 128) && Cout % 32 == 0 &&
+                       Wo <= PB && aligned16 && shifts_aligned4 && N <= 65535 &&
+                       (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31) &&
+                       (size_t)Cout * R * S * Cin < ((size_t)1 << 31) && Cout / 32 <= 65535;
+  if (rows_ok) return MIAIE_CONV_ROWS;
+  const bool fast = Cin % 32 == 0 && Cout % COB == 0 && aligned16 && P < ((size_t)1 << 31) &&
+                    (P + PIX - 1) / PIX < ((size_t)1 << 31) && Cout / COB <= 65535;
+  if (fast) return MIAIE_CONV_IGEMM;
+  return MIAIE_CONV_DIRECT;
+}
+
 int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y,
                      int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad) {
   const int Ho = (H + 2 * pad - R) / stride + 1;
   const int Wo = (Wd + 2 * pad - S) / stride + 1;
   const size_t P = (size_t)N * Ho * Wo;
-  // Row-block kernel (3x3, stride 1, Cin 32 or 64, Wo <= 64).
-  const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64 || Cin == 128) && Cout % 32 == 0 &&
-                       Wo <= PB && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) && aligned(shifts, 4) &&
-                       N <= 65535 && (size_t)N * H * Wd * Cin < ((size_t)1 << 31) &&
-                       (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31);
-  if (rows_ok) {
+  const int kernel = conv2d_kernel_for(N, H, Wd, Cin, Cout, R, S, stride, pad,
+                                       aligned(X, 16) && aligned(W, 16) && aligned(Y, 16), aligned(shifts, 4));
+  if (kernel == MIAIE_CONV_ROWS) {
     if (Cin == 128) return launch_rows<128>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
     if (Cin == 64) return launch_rows<64>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
     return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
   }
-  const bool fast = Cin % 32 == 0 && Cout % COB == 0 && aligned(X, 16) && aligned(W, 16) && aligned(Y, 16) &&
-                    P < ((size_t)1 << 31) && (P + PIX - 1) / PIX < ((size_t)1 << 31);
-  if (fast) {
+  if (kernel == MIAIE_CONV_IGEMM) {
     dim3 grid((unsigned)((P + PIX - 1) / PIX), Cout / COB);
     hipLaunchKernelGGL(conv2d_i8_igemm, grid, dim3(256), 0, ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout,
                        R, S, stride, pad, Ho, Wo);

@@ -116,6 +116,19 @@ MIAIE_API int miaie_plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, miaie_gemm
  * fewer.  cus >= 1; *previous (nullable) receives the old value. */
 MIAIE_API int miaie_plan_set_cus(miaie_ctx* ctx, int cus, int* previous);
 
+/* Which kernel miaie_conv2d_i8_nhwc runs for a shape, given 16-byte aligned
+ * X, W and Y and 4-byte aligned shifts (what miaie_alloc returns).  The
+ * reference's conv exists only as AIE graph configuration
+ * (thirdparty/adf/aie_control.cpp:2554-2559), so there is no reference
+ * counterpart; the choice is exposed so callers and tests can see it.  Needs
+ * no context and no device.
+ * Invalid shapes return MIAIE_EINVAL, as the entry point does. */
+#define MIAIE_CONV_ROWS 0   /* row-block kernel: 3x3, stride 1, Cin 32/64/128, Cout % 32 == 0, Wo <= 64 */
+#define MIAIE_CONV_IGEMM 1  /* implicit-GEMM kernel: Cin % 32 == 0, Cout % 64 == 0 */
+#define MIAIE_CONV_DIRECT 2 /* any shape, one thread per output element */
+MIAIE_API int miaie_plan_conv2d_i8(int N, int H, int W, int Cin, int Cout, int R, int S, int stride, int pad,
+                                   int* kernel);
+
 /* ---- recorded kernel chains --------------------------------------------- */
 
 /* The reference chains kernels through the host: run k1, wait, move k1's

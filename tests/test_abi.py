@@ -6,6 +6,8 @@ import os
 import re
 import subprocess
 
+import pytest
+
 import aiehlc_amd as mi
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -63,3 +65,26 @@ def test_status_codes_match_header():
     for name in ("MIAIE_OK", "MIAIE_EINVAL", "MIAIE_EHIP", "MIAIE_ETIMEDOUT", "MIAIE_ENOMEM", "MIAIE_EUNSUPPORTED"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m and int(m.group(1)) == getattr(mi, name), name
+
+
+def test_conv_planner_keeps_32_bit_offsets_in_range():
+    """The row-block conv kernel indexes X, Y and W with 32-bit offsets; shapes
+    whose weights (Cout * R*S*Cin bytes) reach 2^31 must go to a kernel that
+    indexes in 64 bits.  Host-only: the planner needs no device."""
+    assert mi.plan_conv2d_i8(8, 56, 56, 64, 64) == "rows"            # config 4
+    assert mi.plan_conv2d_i8(1, 1, 1, 128, 64) == "rows"
+    big = (1 << 31) // (9 * 128)                                      # 1864135 channels
+    cout = big - big % 64                                             # multiple of 64 below the bound
+    assert cout * 9 * 128 < 1 << 31
+    assert mi.plan_conv2d_i8(1, 1, 1, 128, cout) == "rows"
+    cout2 = cout + 64                                                 # weights reach 2^31 bytes
+    assert cout2 * 9 * 128 >= 1 << 31
+    assert mi.plan_conv2d_i8(1, 1, 1, 128, cout2) == "igemm"
+    assert mi.plan_conv2d_i8(1, 1, 1, 128, cout2 + 32) == "direct"   # not a multiple of 64
+    # X and Y offsets: a batch whose activations reach 2^31 bytes
+    n_big = (1 << 31) // (56 * 56 * 64) + 1
+    assert mi.plan_conv2d_i8(n_big, 56, 56, 64, 64) == "igemm"
+    assert mi.plan_conv2d_i8(2, 56, 56, 64, 64, stride=2) == "igemm"
+    assert mi.plan_conv2d_i8(1, 5, 5, 4, 8) == "direct"
+    with pytest.raises(mi.MiaieError):
+        mi.plan_conv2d_i8(1, 2, 2, 4, 4, 5, 5, 1, 0)                  # filter larger than the input

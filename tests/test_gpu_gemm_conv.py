@@ -3,8 +3,9 @@ chained int8 MLP, through the miaie C ABI, against the CPU oracle.
 
 Integer paths are compared bit-exactly.  bf16 uses the normwise metric
 max|C - R| / max|R| <= 1e-2 against the fp64 oracle on the same bf16 inputs.
-Full benchmark shapes are checked on row slabs (the oracle computes the same
-rows) plus size-independent properties.
+The integer benchmark shapes (configs 1, 2, 4 and 5) are compared with the
+oracle over every element; bf16 8192^3 on row slabs plus a property that holds
+over the whole output.
 """
 import numpy as np
 import pytest
@@ -107,34 +108,29 @@ def test_gemm_i8_rq_without_debug_output(ctx):
     assert np.array_equal(Yg, oracle.gemm_i8_rq(A, B, 10))
 
 
+def _mismatches(got, want):
+    """The reference's check: count differing elements over the whole output
+    (example/matrixmultiply/aieml_mm.cc:232-245)."""
+    assert got.shape == want.shape, (got.shape, want.shape)
+    return int(np.count_nonzero(got != want))
+
+
 def test_gemm_i8_rq_4096_config(ctx):
-    """Config 2: M=N=K=4096 NN, shift 10.  Bit-exact on a row slab plus 64
-    scattered rows; the int8 output must be the requant of the int32 output
-    everywhere; linearity in A and a row permutation of A check every
-    element."""
+    """Config 2: M=N=K=4096 NN, shift 10, compared with the oracle over every
+    element.  First the benchmarked launch itself (Y only, C_dbg = NULL: the
+    kernel bench.py times), then the launch that also writes the int32
+    accumulators, whose C and Y are compared in full as well."""
     M = N = K = 4096
     _say("gemm_i8_rq 4096^3")
     A = synth.int8((M, K), 1)
     B = synth.int8((K, N), 2)
+    Yo, Co = oracle.gemm_i8_rq(A, B, 10, want_acc=True)
+    Yb, _ = _run_gemm_i8(ctx, A, B, mi.B_NN, 10, False, want_c=False)
+    assert _mismatches(Yb, Yo) == 0
+    del Yb
     Yg, Cg = _run_gemm_i8(ctx, A, B, mi.B_NN, 10, False)
-    assert np.array_equal(Yg, oracle.requant(Cg, 10))
-    Yo, Co = oracle.gemm_i8_rq(A, B, 10, want_acc=True, rows=(0, 256))
-    assert np.array_equal(Cg[:256], Co)
-    assert np.array_equal(Yg[:256], Yo)
-    rows = np.random.default_rng(0).choice(np.arange(256, M), size=64, replace=False)
-    Cr = oracle.gemm_i8(A[rows], B)
-    assert np.array_equal(Cg[rows], Cr)
-    # full-size properties, every element: the Y-only kernel (the benchmarked
-    # one) on a row permutation of A gives the permuted Y of the Y + C run
-    # above; linearity, C(2*A') = 2*C(A') with A' = A>>1 (int8 range kept)
-    perm = np.random.default_rng(4).permutation(M)
-    Yp, _ = _run_gemm_i8(ctx, np.ascontiguousarray(A[perm]), B, mi.B_NN, 10, False, want_c=False)
-    assert np.array_equal(Yp, Yg[perm])
-    del Yp
-    Ah = (A >> 1).astype(np.int8)
-    _, Ch = _run_gemm_i8(ctx, Ah, B, mi.B_NN)
-    _, Ch2 = _run_gemm_i8(ctx, (Ah * 2).astype(np.int8), B, mi.B_NN)
-    assert np.array_equal(Ch2.astype(np.int64), 2 * Ch.astype(np.int64))
+    assert _mismatches(Cg, Co) == 0
+    assert _mismatches(Yg, Yo) == 0
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 1), (64, 64, 64), (37, 70, 45), (256, 256, 32), (512, 256, 512),
@@ -327,11 +323,8 @@ def test_mlp_i8(ctx, shape):
 
 
 def test_mlp_i8_config(ctx):
-    """Config 5: X 2048x4096 -> W1 4096x11008 (rq 11 + ReLU) -> W2 11008x4096 (rq 12).
-    Bit-exact H and Y on a 64-row slab and 32 scattered rows against the
-    oracle; over all rows, a row permutation of X permutes H and Y exactly
-    (each output row depends on its own input row only, so a result that
-    depends on where a row lands in the tile grid shows up here)."""
+    """Config 5: X 2048x4096 -> W1 4096x11008 (rq 11 + ReLU) -> W2 11008x4096
+    (rq 12).  H and Y compared with the oracle over every element."""
     M, K, F, Nout = 2048, 4096, 11008, 4096
     _say("mlp config 5")
     X = synth.int8((M, K), 3)
@@ -342,19 +335,12 @@ def test_mlp_i8_config(ctx):
     ctx.mlp_i8(dX, d1, d2, dH, dY, M, K, F, Nout, 11, 12)
     ctx.wait(120_000)
     Hg, Yg = ctx.download(dH), ctx.download(dY)
-    perm = np.random.default_rng(5).permutation(M)
-    ctx.copy_h2d(dX, np.ascontiguousarray(X[perm]))
-    ctx.mlp_i8(dX, d1, d2, dH, dY, M, K, F, Nout, 11, 12)
-    ctx.wait(120_000)
-    assert np.array_equal(ctx.download(dH), Hg[perm])
-    assert np.array_equal(ctx.download(dY), Yg[perm])
     for b in (dX, d1, d2, dH, dY):
         b.free()
-    assert Hg.min() >= 0  # ReLU
-    rows = np.concatenate([np.arange(64), np.random.default_rng(2).choice(np.arange(64, M), 32, replace=False)])
-    Yo, Ho = oracle.mlp_i8(X[rows], W1, W2, 11, 12, want_h=True)
-    assert np.array_equal(Hg[rows], Ho)
-    assert np.array_equal(Yg[rows], Yo)
+    Yo, Ho = oracle.mlp_i8(X, W1, W2, 11, 12, want_h=True)
+    assert _mismatches(Hg, Ho) == 0
+    assert _mismatches(Yg, Yo) == 0
+    assert Ho.min() >= 0 and Ho.max() > 0  # ReLU, and not all zero
 
 
 def test_fill_i8_matches_host_generator(ctx):

@@ -1,12 +1,13 @@
 """Recorded kernel chains (miaie_graph_*): a chain of entry points recorded
-once and replayed must give, on every replay, exactly what the same calls
-give when run directly on the same inputs.  Eager work (refilling the
-inputs with new seeds) runs between replays, so each replay reads fresh
-buffer contents through the pointers fixed at recording time."""
+once and replayed must give, on every replay, exactly what the CPU oracle
+computes from that replay's inputs.  Eager work (refilling the inputs with
+new seeds) runs between replays, so each replay reads fresh buffer contents
+through the pointers fixed at recording time."""
 import numpy as np
 import pytest
 
 import aiehlc_amd as mi
+import oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -42,7 +43,21 @@ def _refill(ctx, b, seed):
         ctx.fill_i8(b[k], b[k].nbytes, 1000 * seed + i)
 
 
-def test_replays_match_direct_calls(ctx):
+def _oracle_outputs(ctx, b):
+    """What the chain must produce, from the CPU oracle on the inputs the
+    buffers hold (downloaded after the eager refill)."""
+    A, B = ctx.download(b["A"]), ctx.download(b["B"])
+    X, W, S = ctx.download(b["X"]), ctx.download(b["W"]), ctx.download(b["S"])
+    Xm, W1, W2 = ctx.download(b["Xm"]), ctx.download(b["W1"]), ctx.download(b["W2"])
+    Y1 = oracle.gemm_i8_rq(A, B, 10)
+    Y3, H = oracle.mlp_i8(Xm, W1, W2, 11, 12, want_h=True)
+    return {"Y1": Y1, "Y2": oracle.conv2d_nhwc_i8(X, W, S, 1, 1), "H": H, "Y3": Y3, "Y4": Y1}
+
+
+def test_replays_match_the_oracle(ctx):
+    """Every replay's outputs equal the CPU oracle's on that replay's inputs
+    (the reference checks its chains against known answers: multi_tile.cpp:150,
+    seq_full_col.cpp:163), and equal the same calls run directly."""
     b = _buffers(ctx)
     g_out, e_out = _outputs(ctx), _outputs(ctx)
     _refill(ctx, b, 1)
@@ -56,9 +71,11 @@ def test_replays_match_direct_calls(ctx):
             g.launch()
             _chain(ctx, b, e_out)            # the same calls, run directly
             ctx.wait(60_000)
+            want = _oracle_outputs(ctx, b)
             for k in g_out:
-                got, want = ctx.download(g_out[k]), ctx.download(e_out[k])
-                assert np.array_equal(got, want), (replay, k)
+                got = ctx.download(g_out[k])
+                assert np.array_equal(got, want[k]), (replay, k, int(np.count_nonzero(got != want[k])))
+                assert np.array_equal(ctx.download(e_out[k]), want[k]), (replay, k, "direct")
             # the replay really used the new inputs: outputs change with the seed
             if replay == 0:
                 first = ctx.download(g_out["Y1"])
