@@ -74,6 +74,7 @@ _SIGS = {
     "miaie_gemm_bf16_f32": (_i, [_p, _p, _p, _p, _i, _i, _i]),
     "miaie_conv2d_i8_nhwc": (_i, [_p, _p, _p, _p, _p] + [_i] * 9),
     "miaie_mlp_i8": (_i, [_p, _p, _p, _p, _p, _p] + [_i] * 6),
+    "miaie_mlp_i8_noalloc": (_i, [_p, _p, _p, _p, _p] + [_i] * 6),
     "miaie_fill_i8": (_i, [_p, _p, _sz, _u64]),
     "miaie_plan_gemm_i8": (_i, [_p, _i, _i, _i, _p]),
     "miaie_plan_set_cus": (_i, [_p, _i, C.POINTER(_i)]),
@@ -346,6 +347,10 @@ class Context:
 
     def mlp_i8(self, X, W1, W2, H, Y, M, K, F, Nout, s1, s2) -> None:
         self._call("miaie_mlp_i8", _addr(X), _addr(W1), _addr(W2), _addr(H), _addr(Y), M, K, F, Nout, s1, s2)
+
+    def mlp_i8_noalloc(self, X, W1, W2, Y, M, K, F, Nout, s1, s2) -> None:
+        """miaie_mlp_i8 with H in the library's own device array (allocates nothing)."""
+        self._call("miaie_mlp_i8_noalloc", _addr(X), _addr(W1), _addr(W2), _addr(Y), M, K, F, Nout, s1, s2)
 
 
 def version() -> str:

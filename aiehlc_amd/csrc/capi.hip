@@ -109,23 +109,31 @@ extern "C" int miaie_conv2d_i8_nhwc(miaie_ctx* ctx, const int8_t* X, const int8_
   return launch_conv2d_i8(ctx, X, W, shifts, Y, N, H, W_, Cin, Cout, R, S, stride, pad);
 }
 
-extern "C" int miaie_mlp_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W1, const int8_t* W2, int8_t* H,
-                            int8_t* Y, int M, int K, int F, int Nout, int s1, int s2) {
-  int rc = enter(ctx);
-  if (rc) return rc;
-  MIAIE_CHECK_NOT_NULL(ctx, X);
-  MIAIE_CHECK_NOT_NULL(ctx, W1);
-  MIAIE_CHECK_NOT_NULL(ctx, W2);
-  MIAIE_CHECK_NOT_NULL(ctx, H);
-  MIAIE_CHECK_NOT_NULL(ctx, Y);
+namespace miaie {
+
+int mlp_i8_checked(miaie_ctx* ctx, const char* fn, const int8_t* X, const int8_t* W1, const int8_t* W2, int8_t* H,
+                   int8_t* Y, int M, int K, int F, int Nout, int s1, int s2) {
+  int rc;
+  if (X == nullptr || W1 == nullptr || W2 == nullptr || H == nullptr || Y == nullptr)
+    return fail(ctx, MIAIE_EINVAL, "%s: %s is NULL", fn,
+                X == nullptr ? "X" : W1 == nullptr ? "W1" : W2 == nullptr ? "W2" : H == nullptr ? "H" : "Y");
   if (M < 1 || K < 1 || F < 1 || Nout < 1)
-    return fail(ctx, MIAIE_EINVAL, "%s: M=%d K=%d F=%d Nout=%d must all be >= 1", __func__, M, K, F, Nout);
-  if ((rc = check_shift(ctx, __func__, "s1", s1))) return rc;
-  if ((rc = check_shift(ctx, __func__, "s2", s2))) return rc;
+    return fail(ctx, MIAIE_EINVAL, "%s: M=%d K=%d F=%d Nout=%d must all be >= 1", fn, M, K, F, Nout);
+  if ((rc = check_shift(ctx, fn, "s1", s1))) return rc;
+  if ((rc = check_shift(ctx, fn, "s2", s2))) return rc;
   // stage 1: H = relu(rq_s1(X . W1))   (k1 of multi_tile.cpp:39-42)
   rc = launch_gemm_i8(ctx, X, W1, H, nullptr, M, F, K, K, F, F, F, 0, s1, 1);
   if (rc) return rc;
   // stage 2: Y = rq_s2(H . W2), queued behind stage 1 on the same stream
   // (the tile -> tile hand-off of multi_tile.cpp:125-127 without a host trip)
   return launch_gemm_i8(ctx, H, W2, Y, nullptr, M, Nout, F, F, Nout, Nout, Nout, 0, s2, 0);
+}
+
+}  // namespace miaie
+
+extern "C" int miaie_mlp_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W1, const int8_t* W2, int8_t* H,
+                            int8_t* Y, int M, int K, int F, int Nout, int s1, int s2) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  return mlp_i8_checked(ctx, __func__, X, W1, W2, H, Y, M, K, F, Nout, s1, s2);
 }

@@ -16,6 +16,7 @@ struct miaie_ctx {
   hipEvent_t done = nullptr;  // recorded by miaie_wait
   int cus = 256;              // compute units of the device (grid sizing of persistent kernels)
   bool recording = false;     // between miaie_graph_begin and miaie_graph_end
+  void* scratch = nullptr;    // device address of this device's file-scope scratch array (noalloc.hip)
   char err[512] = {0};
 };
 
@@ -38,6 +39,14 @@ int check_launch(miaie_ctx* ctx, const char* kernel);
 int refuse_while_recording(miaie_ctx* ctx, const char* what);
 
 __host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Resolve the device address of the allocation-free entry points' scratch
+// array on ctx->device (current) into ctx->scratch (noalloc.hip).
+int scratch_setup(miaie_ctx* ctx);
+
+// Validated chained MLP over a caller-chosen H (capi.hip).
+int mlp_i8_checked(miaie_ctx* ctx, const char* fn, const int8_t* X, const int8_t* W1, const int8_t* W2, int8_t* H,
+                   int8_t* Y, int M, int K, int F, int Nout, int s1, int s2);
 
 // ---- kernel launchers implemented in the kernel translation units ----
 int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,

@@ -137,6 +137,12 @@ extern "C" int miaie_init_on_stream(miaie_ctx** out, int device, void* stream) {
     delete ctx;
     return rc;
   }
+  if (int rc = scratch_setup(ctx)) {
+    fail(nullptr, rc, "%s", ctx->err);
+    (void)hipEventDestroy(ctx->done);
+    delete ctx;
+    return rc;
+  }
   *out = ctx;
   return MIAIE_OK;
 }

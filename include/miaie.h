@@ -234,6 +234,20 @@ MIAIE_API int miaie_conv2d_i8_nhwc(miaie_ctx* ctx, const int8_t* X, const int8_t
 MIAIE_API int miaie_mlp_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W1, const int8_t* W2,
                            int8_t* H, int8_t* Y, int M, int K, int F, int Nout, int s1, int s2);
 
+/* Allocation-free variant of miaie_mlp_i8.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as miaie_mlp_i8 without H: H lives in a file-scope
+ * device array of MIAIE_MLP_NOALLOC_MAX_H bytes that every GPU the library
+ * runs on holds from miaie_init until the process ends.  M*F above that
+ * returns MIAIE_EINVAL without launching.  The call allocates nothing.  All
+ * calls on one GPU share that GPU's array: calls that overlap on one GPU
+ * (from two streams or contexts) race on it; calls queued on one stream do
+ * not. */
+#define MIAIE_MLP_NOALLOC_MAX_H ((size_t)32 << 20)
+MIAIE_API int miaie_mlp_i8_noalloc(miaie_ctx* ctx, const int8_t* X, const int8_t* W1, const int8_t* W2, int8_t* Y,
+                                   int M, int K, int F, int Nout, int s1, int s2);
+
 /* ---- synthetic inputs --------------------------------------------------- */
 
 /* Fill dst[0..n) with the seeded int8 stream of tensor `tensor_id`
