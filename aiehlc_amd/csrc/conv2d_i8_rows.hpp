@@ -1,0 +1,269 @@
+// Row-block int8 conv2d kernel (device code), shared by the library
+// (conv2d_i8.hip) and the in-kernel clock probe (probes/conv_span.hip).
+//
+// For stride-1 convolutions with Wo <= 64 (instantiated for 3x3 filters and
+// Cin in {32, 64, 128}).  A workgroup owns ROWS output rows of one image (64
+// columns, padded) and one block of WCO output channels, with ROWS * WCO =
+// 128 so that its 8 waves each own 32 pixels x 32 channels.  It stages in LDS
+// once, with every global load of the staging in flight together:
+//   X  the ROWS+R-1 input rows the output rows touch, with the zero padding
+//      columns and rows materialised, [row][col][Cin bytes], 16-byte chunk
+//      c of column col at c ^ xswz(col) (conflict-free fragment reads);
+//   W  the WCO output channels' OHWI rows, pitch R*S*Cin + 16 bytes.
+// Each wave then runs the whole k = (r, s, ci) reduction from LDS (one
+// v_mfma_i32_32x32x32_i8 per 32-wide k-step, fully unrolled), so there is no
+// im2col buffer and no cross-wave reduction.  The requantized int8 results
+// go through a third LDS region and leave as 16-byte stores of whole output
+// pixels' channel runs: the workgroup's ROWS x Wo x WCO block is one
+// contiguous run of Y when WCO == Cout.  (Stored straight from the
+// accumulators, each lane wrote 4-byte pieces of 8 different 64-byte pixel
+// runs, and the lines left partially written in L2 made the end of every
+// launch 0.3-0.4 us longer.)
+//
+// Tile order: with N a multiple of 8 the grid is (8, row blocks, N/8 *
+// channel blocks) and workgroup (x, y, z) takes image 8*(z mod N/8) + x.
+// Workgroups are dealt round-robin to the 8 XCDs in linear order, so XCD x
+// runs every workgroup of its images and the ROWS+2 staged rows of
+// neighbouring row blocks, which overlap in 2 rows, are fetched into its L2
+// once (measured: 1.98 MB read per launch at config 4 against 3.52 MB with
+// neighbouring row blocks on different XCDs; X + W is 1.64 MB).  Otherwise
+// the grid is (row blocks, channel blocks, N).
+#pragma once
+
+#include "miaie_internal.hpp"
+
+namespace miaie {
+namespace conv {
+
+constexpr int PB = 64;  // output columns per row (padded)
+
+template <int CIN>
+__device__ __forceinline__ int xswz(int col) {
+  return (col * CIN / 256) & (CIN / 16 - 1);
+}
+
+template <int R, int S, int CIN, int ROWS, int WCO>
+struct RowsGeom {
+  static_assert(ROWS * WCO == 128 && WCO % 32 == 0, "8 waves of 32 pixels x 32 channels");
+  static constexpr int NWC = WCO / 32;                      // 32-channel blocks per workgroup
+  static constexpr int XR = ROWS + R - 1, XC = PB + S - 1;  // staged input rows / columns
+  static constexpr int NCH = CIN / 16;                      // 16-byte chunks per pixel
+  // X staging map: one pass covers RPP whole rows of the first PB staged
+  // columns (thread -> chunk tid % NCH of column tid / NCH % PB), XQ passes
+  // cover the XR rows, and one more load per thread (the first XE threads)
+  // covers the last S - 1 columns of every row.
+  static constexpr int RPP = 512 / (PB * NCH);              // rows per pass
+  static constexpr int XQ = (XR + RPP - 1) / RPP;           // passes
+  static constexpr int XE = XR * (XC - PB) * NCH;           // chunks of the last S - 1 columns
+  static constexpr int RSC = R * S * CIN, WP = RSC + 16;    // weight row length / LDS pitch
+  static constexpr int WTOT = WCO * RSC / 16;               // W chunks
+  static constexpr int WQ = (WTOT + 511) / 512;
+  static constexpr int WREM = WTOT - 512 * (WQ - 1);        // W chunks of the last pass
+  static_assert(512 % (PB * NCH) == 0 && XE <= 512, "row-block conv staging map");
+  static constexpr int X_BYTES = XR * XC * CIN;
+  static constexpr int W_BYTES = WCO * WP;
+  static constexpr int YP = WCO + 16;                       // LDS pitch of one staged output pixel
+  static constexpr int Y_BYTES = ROWS * PB * YP;
+  static constexpr int CPP = WCO / 16;                      // 16-byte output chunks per pixel
+  static_assert(ROWS * PB * CPP == 512, "one 16-byte output chunk per thread");
+  static constexpr int LDS = X_BYTES + W_BYTES + Y_BYTES;
+  static constexpr int T = R * S * CIN / 32;                // 32-wide k-steps
+  static_assert(LDS <= 163840, "row-block conv LDS budget (160 KiB per workgroup on gfx950)");
+};
+
+// Clock probe records per wave (TIMED instantiations only): shader clock at
+// the start, after the staging barrier, after the MFMA loop and at the end,
+// then the 100 MHz wall clock at the start and the end.
+constexpr int PROBE_WORDS = 6;
+
+// xg: 0 for the (row blocks, channel blocks, N) grid, else N / 8 for the
+// image-per-XCD grid.  probe: PROBE_WORDS words per wave (TIMED only).
+template <int R, int S, int CIN, int ROWS, int WCO, bool TIMED>
+__global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
+                                                      const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
+                                                      int H, int Wd, int Cout, int pad, int Ho, int Wo, int xg,
+                                                      unsigned long long* __restrict__ probe) {
+  using G = RowsGeom<R, S, CIN, ROWS, WCO>;
+  __shared__ __attribute__((aligned(16))) int8_t smem[G::LDS];
+  unsigned long long t0 = 0, r0 = 0;
+  if constexpr (TIMED) {
+    t0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, fh = lane >> 5;
+  int n, rb, cb;
+  if (xg) {
+    rb = blockIdx.y;
+    const int z = blockIdx.z;
+    cb = xg == 1 ? z : z / xg;
+    n = 8 * (z - cb * xg) + blockIdx.x;
+  } else {
+    rb = blockIdx.x;
+    cb = blockIdx.y;
+    n = blockIdx.z;
+  }
+  const int ho0 = rb * ROWS;
+  const int co0 = cb * WCO;
+  int8_t* const xs = smem;
+  int8_t* const ws = smem + G::X_BYTES;
+  int8_t* const ys = smem + G::X_BYTES + G::W_BYTES;
+
+  // wave: output row rr, pixels 32pb .. +32, channels 32wc .. +32
+  const int wc = wave % G::NWC, pb = (wave / G::NWC) & 1, rr = wave / (2 * G::NWC);
+
+  // this lane's 16 output channels' shifts (4 per dword), loaded up front so
+  // their latency hides under the staging
+  uint32_t sh4[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) sh4[g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc + 8 * g + 4 * fh);
+
+  // ---- stage X (zero outside the image) and W.  Every load is issued before
+  // any is waited for: positions outside the image load the nearest chunk
+  // inside it and are zeroed by a select afterwards (a branch around the load would
+  // make the zero write wait for the load in flight to the same registers).
+  // Offsets are 32-bit from the tensor base: the launcher keeps X, W and Y
+  // below 2^31 bytes.
+  const int xc = tid % G::NCH, xcol = (tid / G::NCH) % PB, xrow = tid / (G::NCH * PB);
+  // (threads past XE repeat an earlier thread's chunk: the same value to the
+  // same LDS address, so the load and the write need no branch)
+  const int et = tid % G::XE;
+  const int ec = et % G::NCH, ecol = PB + (et / G::NCH) % (G::XC - PB), erow = et / (G::NCH * (G::XC - PB));
+  auto x_off = [&](int row, int col, int c, bool& in) -> uint32_t {
+    const int hi = ho0 + row - pad, wi = col - pad;
+    in = (unsigned)hi < (unsigned)H && (unsigned)wi < (unsigned)Wd;
+    // clamped into the image: a valid address without a branch
+    const int hc = min(max(hi, 0), H - 1), wcl = min(max(wi, 0), Wd - 1);
+    return (uint32_t)(((n * H + hc) * Wd + wcl) * CIN + 16 * c);
+  };
+  v4i xv[G::XQ], xe, wv[G::WQ];
+  bool xin[G::XQ], ein;
+  // (a pass that runs past the last staged row repeats that row's chunks)
+  auto xrow_of = [&](int u) { return min(G::RPP * u + xrow, G::XR - 1); };
+#pragma unroll
+  for (int u = 0; u < G::XQ; ++u)
+    xv[u] = *reinterpret_cast<const v4i*>(X + x_off(xrow_of(u), xcol, xc, xin[u]));
+  xe = *reinterpret_cast<const v4i*>(X + x_off(erow, ecol, ec, ein));
+  // (threads past the end of the last W pass repeat that pass's chunks)
+  auto wq_of = [&](int u) { return u < G::WQ - 1 ? tid + 512 * u : 512 * (G::WQ - 1) + tid % G::WREM; };
+#pragma unroll
+  for (int u = 0; u < G::WQ; ++u) wv[u] = *reinterpret_cast<const v4i*>(W + (uint32_t)(co0 * G::RSC + 16 * wq_of(u)));
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
+
+  // The accumulators start at the rounding term 2^(s-1) of their channel
+  // (|acc| <= R*S*CIN * 2^14 < 2^30 keeps acc + 2^30 inside int32), so the
+  // epilogue only shifts and saturates.  Computed here, while the staging
+  // loads are in flight (the shifts were issued first).
+  v16i acc;
+  int smin = 31;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int sc = (sh4[g] >> (8 * tt)) & 31;
+      acc[4 * g + tt] = (int)((1u << sc) >> 1);
+      smin = min(smin, sc);
+    }
+  const bool hi_form = __builtin_amdgcn_ballot_w64(smin < 8) == 0;  // every shift of the wave >= 8
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto x_put = [&](int row, int col, int c, bool in, v4i v) {
+    *reinterpret_cast<v4i*>(xs + (row * G::XC + col) * CIN + ((c ^ xswz<CIN>(col)) << 4)) = in ? v : v4i{0};
+  };
+#pragma unroll
+  for (int u = 0; u < G::XQ; ++u) x_put(xrow_of(u), xcol, xc, xin[u], xv[u]);
+  x_put(erow, ecol, ec, ein, xe);
+#pragma unroll
+  for (int u = 0; u < G::WQ; ++u) {
+    const int q = wq_of(u);
+    *reinterpret_cast<v4i*>(ws + (q / (G::RSC / 16)) * G::WP + 16 * (q % (G::RSC / 16))) = wv[u];
+  }
+  __syncthreads();
+  unsigned long long t1 = 0;
+  if constexpr (TIMED) t1 = __builtin_amdgcn_s_memtime();
+
+  const int px = 32 * pb + fr;
+  const int8_t* wrow = ws + (32 * wc + fr) * G::WP + 16 * fh;
+#pragma unroll
+  for (int t = 0; t < G::T; ++t) {
+    const int cib = t % (CIN / 32), rs = t / (CIN / 32);
+    const int r = rs / S, s = rs % S;
+    const int col = px + s;
+    const v4i xf = *reinterpret_cast<const v4i*>(xs + ((rr + r) * G::XC + col) * CIN +
+                                                 (((2 * cib + fh) ^ xswz<CIN>(col)) << 4));
+    const v4i wf = *reinterpret_cast<const v4i*>(wrow + 32 * t);
+    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, xf, acc, 0, 0, 0);
+  }
+  unsigned long long t2 = 0;
+  if constexpr (TIMED) t2 = __builtin_amdgcn_s_memtime();
+
+  // ---- requant (per channel) into the Y region.  acc[4g + tt]: channel
+  // 32wc + 8g + 4*(lane/32) + tt, pixel px: four consecutive channels of one
+  // pixel per dword.  (Padding columns px >= Wo land in LDS and are never
+  // read back.)
+  int8_t* const yl = ys + (rr * PB + px) * G::YP + 32 * wc + 4 * fh;
+  if (hi_form) {
+    // s >= 8: y is the high byte of sat_int16(acc >> (s - 8)) (floor
+    // shifts compose; saturating at 16 bits clamps the high byte exactly
+    // at -128 and 127), 7 instructions per 4 channels
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t sm8 = sh4[g] - 0x08080808u;  // bytewise s - 8 (no borrow: every byte >= 8)
+      const int u0 = acc[4 * g] >> (sm8 & 31), u1 = acc[4 * g + 1] >> ((sm8 >> 8) & 31);
+      const int u2 = acc[4 * g + 2] >> ((sm8 >> 16) & 31), u3 = acc[4 * g + 3] >> ((sm8 >> 24) & 31);
+      const uint32_t p01 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(u0, u1));
+      const uint32_t p23 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(u2, u3));
+      *reinterpret_cast<uint32_t*>(yl + 8 * g) = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int q = min(max(acc[4 * g + tt] >> ((sh4[g] >> (8 * tt)) & 31), -128), 127);
+        packed |= (uint32_t)(q & 0xFF) << (8 * tt);
+      }
+      *reinterpret_cast<uint32_t*>(yl + 8 * g) = packed;
+    }
+  }
+  __syncthreads();
+  // ---- store: thread -> output pixel p of the ROWS x Wo block (row-major),
+  // 16-byte channel chunk c: consecutive threads write consecutive 16 bytes
+  // of Y (one contiguous run per pixel, and per row block when WCO == Cout)
+  {
+    const int p = tid / G::CPP, c = tid % G::CPP;
+    int prow = 0;
+#pragma unroll
+    for (int k = 1; k < ROWS; ++k) prow += p >= k * Wo;
+    const int pcol = p - prow * Wo;
+    if (pcol < Wo && ho0 + prow < Ho) {
+      const v4i v = *reinterpret_cast<const v4i*>(ys + (prow * PB + pcol) * G::YP + 16 * c);
+      *reinterpret_cast<v4i*>(Y + (uint32_t)(((n * Ho + ho0 + prow) * Wo + pcol) * Cout + co0 + 16 * c)) = v;
+    }
+  }
+  if constexpr (TIMED) {
+    const unsigned long long t3 = __builtin_amdgcn_s_memtime(), r3 = __builtin_amdgcn_s_memrealtime();
+    const unsigned long long rec[PROBE_WORDS] = {t0, t1, t2, t3, r0, r3};
+    unsigned long long v = 0;
+#pragma unroll
+    for (int i = 0; i < PROBE_WORDS; ++i) v = lane == i ? rec[i] : v;
+    const size_t wg = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    if (lane < PROBE_WORDS) probe[(wg * 8 + wave) * PROBE_WORDS + lane] = v;
+  }
+}
+
+// Grid and launch of the row-block kernel (shapes already checked by the
+// caller: rows_ok in conv2d_kernel_for).
+template <int CIN, int ROWS, int WCO, bool TIMED>
+inline void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
+                           int H, int Wd, int Cout, int pad, int Ho, int Wo, unsigned long long* probe = nullptr) {
+  const unsigned rbs = (unsigned)((Ho + ROWS - 1) / ROWS), cbs = (unsigned)(Cout / WCO);
+  const bool by_xcd = N % 8 == 0 && rbs <= 65535 && (size_t)(N / 8) * cbs <= 65535;
+  const dim3 grid = by_xcd ? dim3(8, rbs, (unsigned)(N / 8) * cbs) : dim3(rbs, cbs, (unsigned)N);
+  hipLaunchKernelGGL((conv2d_i8_rows<3, 3, CIN, ROWS, WCO, TIMED>), grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd,
+                     Cout, pad, Ho, Wo, by_xcd ? N / 8 : 0, probe);
+}
+
+}  // namespace conv
+}  // namespace miaie

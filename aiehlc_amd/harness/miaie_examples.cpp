@@ -15,7 +15,8 @@
 //   seq_full_col    example/multi/seq_full_col.cpp:65-181 (8 stages, expects 23)
 //   vek385          example/multi/vek385_verification.cpp:104-157 (3x3 A.A per tile)
 //   gemm M N K s    int8 GEMM + requant (benchmark configs), golden on sampled rows
-//   conv            int8 3x3 conv2d, benchmark config 4, golden on one image
+//   conv [reps]     int8 3x3 conv2d, benchmark config 4, golden on one image;
+//                   with reps, then times reps back-to-back calls
 //   mlp M K F N     chained int8 MLP, golden on sampled rows
 #include <chrono>
 #include <cstdio>
@@ -201,7 +202,7 @@ int run_gemm(miaie::Context& ctx, int M, int N, int K, int shift) {
   return report(mismatches, "gemm");
 }
 
-int run_conv(miaie::Context& ctx) {
+int run_conv(miaie::Context& ctx, int reps) {
   const int Nb = 8, H = 56, Wd = 56, C = 64, Co = 64;
   const std::vector<int8_t> X = seeded_i8((size_t)Nb * H * Wd * C, 3), W = seeded_i8((size_t)Co * 9 * C, 4);
   const std::vector<uint8_t> sh = seeded_shifts(Co, 7);
@@ -228,6 +229,17 @@ int run_conv(miaie::Context& ctx) {
           }
         mismatches += Y[(((size_t)n * H + h) * Wd + w) * Co + co] != rq(acc, sh[co], false);
       }
+  if (reps > 0) {
+    // back-to-back calls of the C entry point from C++, after as many
+    // untimed ones: host launch work and device time overlap, so this is the
+    // device's time per convolution unless the host is slower
+    for (int i = 0; i < reps; ++i) miaie::conv2d_i8(dX, dW, dS, dY, miaie::ConvShape{Nb, H, Wd, C, Co}, ctx);
+    if (!ctx.wait(kDeadlineMs)) return 2;
+    const auto t0 = clk::now();
+    for (int i = 0; i < reps; ++i) miaie::conv2d_i8(dX, dW, dS, dY, miaie::ConvShape{Nb, H, Wd, C, Co}, ctx);
+    if (!ctx.wait(kDeadlineMs)) return 2;
+    printf("conv2d back-to-back: %.3f us per call over %d calls\n", us_since(t0) / reps, reps);
+  }
   return report(mismatches, "conv2d");
 }
 
@@ -262,7 +274,7 @@ int run_mlp(miaie::Context& ctx, int M, int K, int F, int Nout) {
 int usage() {
   fprintf(stderr,
           "usage: miaie_examples mm [n 8|16] [base] | perf | nokernelload | multi_tile | seq_full_col | vek385 |\n"
-          "                      gemm M N K shift | conv | mlp M K F N\n");
+          "                      gemm M N K shift | conv [reps] | mlp M K F N\n");
   return 64;
 }
 
@@ -286,7 +298,7 @@ int main(int argc, char** argv) {
     if (cmd == "seq_full_col") return run_chain(ctx, std::vector<int32_t>(8, 1), 23, "seq_full_col");
     if (cmd == "vek385") return run_vek385(ctx);
     if (cmd == "gemm") return run_gemm(ctx, arg(2, 4096), arg(3, 4096), arg(4, 4096), arg(5, 10));
-    if (cmd == "conv") return run_conv(ctx);
+    if (cmd == "conv") return run_conv(ctx, arg(2, 0));
     if (cmd == "mlp") return run_mlp(ctx, arg(2, 256), arg(3, 4096), arg(4, 11008), arg(5, 4096));
     return usage();
   } catch (const miaie::Error& e) {

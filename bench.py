@@ -57,6 +57,7 @@ PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_rq_4096_traffic.txt")
 CEILING_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "mfma_ceiling")
 FLOOR_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "launch_floor")
+CONV_SPAN_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "conv_span")
 FLOWS_EXE = os.path.join(ROOT, "aiehlc_amd", "harness", "xaie_flows")
 METRIC = "int8 GEMM TOPS (% MFMA peak) at 4096^3; int8 conv2d 3x3 GOPS; vs host CPU"
 
@@ -254,6 +255,18 @@ def probe_json(exe: str) -> dict | None:
     return json.loads(r.stdout)
 
 
+def cpp_conv_loop(reps: int) -> float | None:
+    """us per back-to-back call of the config-4 conv from the C++ harness."""
+    exe = os.path.join(ROOT, "aiehlc_amd", "harness", "miaie_examples")
+    if not os.path.exists(exe):
+        return None
+    r = subprocess.run([exe, "conv", str(reps)], capture_output=True, text=True, timeout=120)
+    m = re.search(r"back-to-back: ([0-9.]+) us per call", r.stdout)
+    if r.returncode != 0 or not m:
+        return None
+    return float(m.group(1))
+
+
 def mfma_ceiling() -> dict | None:
     return probe_json(CEILING_EXE)
 
@@ -328,6 +341,147 @@ def vendor_library(steps: int) -> dict:
     return out
 
 
+def extra_conv(ctx, timer, args) -> dict:
+    """Config 4: int8 conv2d 3x3, N=8 56x56 Cin=Cout=64."""
+    import aiehlc_amd as mi
+
+    Nb, H, W, Ci, Co = 8, 56, 56, 64, 64
+    dX, dW, dS, dYc = (ctx.empty((Nb, H, W, Ci), np.int8), ctx.empty((Co, 3, 3, Ci), np.int8),
+                       ctx.upload(mi.synth.shifts(Co, 7)), ctx.empty((Nb, H, W, Co), np.int8))
+    ctx.fill_i8(dX, Nb * H * W * Ci, 3)
+    ctx.fill_i8(dW, Co * 9 * Ci, 4)
+    conv1 = lambda: ctx.conv2d_i8_nhwc(dX, dW, dS, dYc, Nb, H, W, Ci, Co, 3, 3, 1, 1)
+    ms_c = timed(ctx, timer, conv1, max(args.steps, 200), args.warmup)
+    # single launches, hot and cold: "cold" writes 512 MiB first (twice the
+    # 256 MB MALL; the L2s start every kernel invalidated anyway), so the
+    # convolution reads X and W from HBM
+    flush_bytes = 512 << 20
+    dF = ctx.alloc(flush_bytes)
+    us_hot1 = single_launch_us(ctx, timer, conv1, 50)
+    us_cold1 = single_launch_us(ctx, timer, conv1, 50, lambda: ctx.fill_i8(dF, flush_bytes, 11))
+    dF.free()
+    # the same convolution recorded 20 times into one graph (miaie_graph_*):
+    # replays have no host launch gap between the convolutions
+    chain = 20
+    with ctx.record() as g:
+        for _ in range(chain):
+            conv1()
+    ms_cg = timed(ctx, timer, g.launch, max(10, args.steps // 5), 2) / chain
+    g.destroy()
+    for b in (dX, dW, dS, dYc):
+        b.free()
+    conv_ops = 2.0 * Nb * H * W * Co * Ci * 9
+    conv_bytes = Nb * H * W * Ci + Co * 9 * Ci + Co + Nb * H * W * Co
+    roof = min(PEAK_INT8_TOPS, conv_ops / conv_bytes * PEAK_HBM_GBS / 1e3)
+    # the same convolution called back to back through the C ABI from the C++
+    # harness (the Python loop above adds a ctypes call per launch, which can
+    # be slower than the device)
+    cpp = cpp_conv_loop(3000)
+    # the kernel's own execution time from in-kernel clocks (the same kernel
+    # template, instantiated with clock records, in its own process)
+    span = probe_json(CONV_SPAN_EXE)
+    if cpp is not None:
+        us_c, step_from = cpp, ("C++ harness, 3000 back-to-back miaie_conv2d_i8_nhwc calls "
+                                "(aiehlc_amd/harness/miaie_examples conv 3000)")
+    else:
+        us_c, step_from = ms_c * 1e3, "Python loop over the ctypes binding, HIP events"
+    if isinstance(span, dict) and "span_us" in span:
+        s_us = span["span_us"]
+        span["alg_GBps"] = round(conv_bytes / (s_us * 1e-6) / 1e9, 1)
+        span["frac"] = round(conv_ops / (s_us * 1e-6) / 1e12 / roof, 4)
+    return {
+        "config": "N=8 H=W=56 Cin=Cout=64 3x3 stride 1 pad 1, NHWC x OHWI, per-channel shift in [8,12]",
+        "kernel": "conv2d_i8_rows<3,3,64,2,64> (2 output rows x 64 channels per workgroup, image-per-XCD grid)",
+        "us_per_step": round(us_c, 3),
+        "us_per_step_from": step_from,
+        "gops": round(conv_ops / (us_c * 1e-6) / 1e9, 1),
+        "alg_GBps": round(conv_bytes / (us_c * 1e-6) / 1e9, 1),
+        "roofline": {"bound": "hbm", "achieved": round(conv_bytes / (us_c * 1e-6) / 1e9, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "alg_bytes": conv_bytes,
+                     "roof_tops": round(roof, 1),
+                     "frac": round(conv_ops / (us_c * 1e-6) / 1e12 / roof, 4)},
+        "python_loop_us_per_step": round(ms_c * 1e3, 3),
+        "graph_chain": {"convs_per_replay": chain, "us_per_conv": round(ms_cg * 1e3, 3),
+                        "gops": round(conv_ops / (ms_cg * 1e-3) / 1e9, 1),
+                        "frac": round(conv_ops / (ms_cg * 1e-3) / 1e12 / roof, 4)},
+        "single_launch_us": {"hot": round(us_hot1, 3), "cold_hbm": round(us_cold1, 3),
+                             "how": "median of 50 launches, each alone between two events on a drained stream; "
+                                    "cold_hbm writes 512 MiB before each launch (outside the events)"},
+        "in_kernel": span,
+        "note": "events bracket back-to-back launches, so us_per_step includes the command processor's work "
+                "between launches (an empty kernel of the same grid: extras.launch_floor); in_kernel.span_us is "
+                "the first wave's start to the last wave's end by the GPU's wall clock "
+                "(aiehlc_amd/probes/conv_span); graph_chain replays 20 recorded convolutions per launch",
+    }
+
+
+def extra_m_shard(ctx, timer, args) -> dict:
+    """One GPU's share of the 4096^3 GEMM sharded 8 and 16 ways over M: the
+    planner picks 128x128 tiles so the grid still covers the CUs."""
+    import aiehlc_amd as mi
+
+    N = K = 4096
+    shard = {}
+    for Ms in (512, 256):
+        dAs, dBs, dYs = ctx.empty((Ms, K), np.int8), ctx.empty((K, N), np.int8), ctx.empty((Ms, N), np.int8)
+        ctx.fill_i8(dAs, Ms * K, 1)
+        ctx.fill_i8(dBs, K * N, 2)
+        ms_s = timed(ctx, timer, lambda: ctx.gemm_i8_rq(dAs, dBs, dYs, Ms, N, K, 10, False, None, mi.B_NN),
+                     args.steps, args.warmup)
+        sops = 2.0 * Ms * N * K
+        shard[f"M{Ms}"] = {"shape": [Ms, N, K], "plan": ctx.plan_gemm_i8(Ms, N, K), "us": round(ms_s * 1e3, 2),
+                           "tops": round(sops / (ms_s * 1e-3) / 1e12, 1),
+                           "frac_of_peak": round(sops / (ms_s * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+        for b in (dAs, dBs, dYs):
+            b.free()
+    return shard
+
+
+def extra_bf16(ctx, timer, args) -> dict:
+    """Config 3: bf16 8192^3, fp32 accumulate and output."""
+    import aiehlc_amd as mi
+
+    Mb = 8192
+    dAb, dBb, dCb = (ctx.empty((Mb, Mb), np.uint16), ctx.empty((Mb, Mb), np.uint16),
+                     ctx.empty((Mb, Mb), np.float32))
+    ctx.copy_h2d(dAb, mi.synth.bf16_normal((Mb, Mb), 1, 1.0 / np.sqrt(Mb)))
+    ctx.copy_h2d(dBb, mi.synth.bf16_normal((Mb, Mb), 2, 1.0 / np.sqrt(Mb)))
+    bf16_step = lambda: ctx.gemm_bf16_f32(dAb, dBb, dCb, Mb, Mb, Mb)
+    settle(ctx, bf16_step, args.settle)
+    n_b = max(20, args.steps // 10)
+    ms_b = timed(ctx, timer, bf16_step, n_b, 5)
+    for b in (dAb, dBb, dCb):
+        b.free()
+    tf = 2.0 * Mb ** 3 / (ms_b * 1e-3) / 1e12
+    return {"kernel": "gemm_bf16_pair", "ms_per_step": round(ms_b, 4),
+            "tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "timed_launches": n_b, "warmup": 5,
+            "how": f"{args.settle} s of untimed launches, 5 warm-ups, then {n_b} back-to-back "
+                   "launches between two events"}
+
+
+def extra_mlp(ctx, timer, args) -> dict:
+    """Config 5: the chained int8 MLP 2048x4096 -> 11008 -> 4096."""
+    Mm, Km, Fm, Nm = 2048, 4096, 11008, 4096
+    dXm, d1, d2 = ctx.empty((Mm, Km), np.int8), ctx.empty((Km, Fm), np.int8), ctx.empty((Fm, Nm), np.int8)
+    dH, dYm = ctx.empty((Mm, Fm), np.int8), ctx.empty((Mm, Nm), np.int8)
+    ctx.fill_i8(dXm, Mm * Km, 3)
+    ctx.fill_i8(d1, Km * Fm, 5)
+    ctx.fill_i8(d2, Fm * Nm, 6)
+    ms_m = timed(ctx, timer, lambda: ctx.mlp_i8(dXm, d1, d2, dH, dYm, Mm, Km, Fm, Nm, 11, 12),
+                 max(5, args.steps // 2), 2)
+    for b in (dXm, d1, d2, dH, dYm):
+        b.free()
+    mops = 2.0 * 2 * Mm * Km * Fm
+    return {"kernel": "gemm_i8_pipe2<256, 128, 4, NN, Y_HI_RELU> + gemm_i8_pipe2<256, 128, 4, NN, Y_HI>",
+            "ms_per_step": round(ms_m, 4),
+            "tops": round(mops / (ms_m * 1e-3) / 1e12, 1),
+            "frac_of_peak": round(mops / (ms_m * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+
+
+EXTRAS = {"conv": extra_conv, "m_shard": extra_m_shard, "bf16": extra_bf16, "mlp": extra_mlp}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -338,6 +492,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extras", action="store_true", help="headline workload only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", choices=sorted(EXTRAS), default=None,
+                    help="run one extra workload alone and print its JSON (for profiling it by itself)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run miaie_copy_d2d of MIB MiB, --steps times (HBM counter calibration)")
     args = ap.parse_args()
@@ -360,6 +516,11 @@ def main() -> int:
         ctx.close()
         return 0
 
+    if args.only:
+        print(json.dumps({"only": args.only, args.only: EXTRAS[args.only](ctx, timer, args)}), flush=True)
+        ctx.close()
+        return 0
+
     # ---- headline: int8 GEMM + requant, 4096^3 NN, shift 10
     M = N = K = 4096
     dA, dB, dY = ctx.empty((M, K), np.int8), ctx.empty((K, N), np.int8), ctx.empty((M, N), np.int8)
@@ -379,105 +540,10 @@ def main() -> int:
 
     extras = {}
     if not args.no_extras:
-        # config 4: int8 conv2d 3x3
-        Nb, H, W, Ci, Co = 8, 56, 56, 64, 64
-        dX, dW, dS, dYc = (ctx.empty((Nb, H, W, Ci), np.int8), ctx.empty((Co, 3, 3, Ci), np.int8),
-                           ctx.upload(mi.synth.shifts(Co, 7)), ctx.empty((Nb, H, W, Co), np.int8))
-        ctx.fill_i8(dX, Nb * H * W * Ci, 3)
-        ctx.fill_i8(dW, Co * 9 * Ci, 4)
-        ms_c = timed(ctx, timer, lambda: ctx.conv2d_i8_nhwc(dX, dW, dS, dYc, Nb, H, W, Ci, Co, 3, 3, 1, 1),
-                     max(args.steps, 200), args.warmup)
-        # single launches, hot and cold: "cold" writes 512 MiB first (twice the
-        # 256 MB MALL; the L2s start every kernel invalidated anyway), so the
-        # convolution reads X and W from HBM
-        conv1 = lambda: ctx.conv2d_i8_nhwc(dX, dW, dS, dYc, Nb, H, W, Ci, Co, 3, 3, 1, 1)
-        flush_bytes = 512 << 20
-        dF = ctx.alloc(flush_bytes)
-        us_hot1 = single_launch_us(ctx, timer, conv1, 50)
-        us_cold1 = single_launch_us(ctx, timer, conv1, 50, lambda: ctx.fill_i8(dF, flush_bytes, 11))
-        dF.free()
-        # the same convolution recorded 20 times into one graph (miaie_graph_*):
-        # replays have no host launch gap between the convolutions
-        chain = 20
-        with ctx.record() as g:
-            for _ in range(chain):
-                ctx.conv2d_i8_nhwc(dX, dW, dS, dYc, Nb, H, W, Ci, Co, 3, 3, 1, 1)
-        ms_cg = timed(ctx, timer, g.launch, max(10, args.steps // 5), 2) / chain
-        g.destroy()
-        conv_ops = 2.0 * Nb * H * W * Co * Ci * 9
-        conv_bytes = Nb * H * W * Ci + Co * 9 * Ci + Co + Nb * H * W * Co
-        roof = min(PEAK_INT8_TOPS, conv_ops / conv_bytes * PEAK_HBM_GBS / 1e3)
-        extras["conv2d_3x3"] = {
-            "config": "N=8 H=W=56 Cin=Cout=64 3x3 stride 1 pad 1, NHWC x OHWI, per-channel shift in [8,12]",
-            "kernel": "conv2d_i8_rows<3,3,64,2,64> (2 output rows x 64 channels per workgroup)",
-            "us_per_step": round(ms_c * 1e3, 3),
-            "gops": round(conv_ops / (ms_c * 1e-3) / 1e9, 1),
-            "alg_GBps": round(conv_bytes / (ms_c * 1e-3) / 1e9, 1),
-            "roofline": {"bound": "hbm", "achieved": round(conv_bytes / (ms_c * 1e-3) / 1e9, 1),
-                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "alg_bytes": conv_bytes,
-                         "roof_tops": round(roof, 1),
-                         "frac": round(conv_ops / (ms_c * 1e-3) / 1e12 / roof, 4)},
-            "graph_chain": {"convs_per_replay": chain, "us_per_conv": round(ms_cg * 1e3, 3),
-                            "gops": round(conv_ops / (ms_cg * 1e-3) / 1e9, 1),
-                            "frac": round(conv_ops / (ms_cg * 1e-3) / 1e12 / roof, 4)},
-            "single_launch_us": {"hot": round(us_hot1, 3), "cold_hbm": round(us_cold1, 3),
-                                 "how": "median of 50 launches, each alone between two events on a drained stream; "
-                                        "cold_hbm writes 512 MiB before each launch (outside the events)"},
-            "note": "events bracket back-to-back launches, so us_per_step includes the gap between launches; "
-                    "graph_chain replays 20 recorded convolutions per launch",
-        }
-        for b in (dX, dW, dS, dYc):
-            b.free()
-        # one GPU's share of the 4096^3 GEMM sharded 8 and 16 ways over M: the
-        # planner picks 128x128 tiles so the grid still covers the CUs
-        shard = {}
-        for Ms in (512, 256):
-            dAs, dBs, dYs = ctx.empty((Ms, K), np.int8), ctx.empty((K, N), np.int8), ctx.empty((Ms, N), np.int8)
-            ctx.fill_i8(dAs, Ms * K, 1)
-            ctx.fill_i8(dBs, K * N, 2)
-            ms_s = timed(ctx, timer, lambda: ctx.gemm_i8_rq(dAs, dBs, dYs, Ms, N, K, 10, False, None, mi.B_NN),
-                         args.steps, args.warmup)
-            sops = 2.0 * Ms * N * K
-            shard[f"M{Ms}"] = {"shape": [Ms, N, K], "plan": ctx.plan_gemm_i8(Ms, N, K), "us": round(ms_s * 1e3, 2),
-                               "tops": round(sops / (ms_s * 1e-3) / 1e12, 1),
-                               "frac_of_peak": round(sops / (ms_s * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
-            for b in (dAs, dBs, dYs):
-                b.free()
-        extras["gemm_i8_m_shard"] = shard
-        # config 3: bf16 8192^3
-        Mb = 8192
-        dAb, dBb, dCb = (ctx.empty((Mb, Mb), np.uint16), ctx.empty((Mb, Mb), np.uint16),
-                         ctx.empty((Mb, Mb), np.float32))
-        ctx.copy_h2d(dAb, mi.synth.bf16_normal((Mb, Mb), 1, 1.0 / np.sqrt(Mb)))
-        ctx.copy_h2d(dBb, mi.synth.bf16_normal((Mb, Mb), 2, 1.0 / np.sqrt(Mb)))
-        bf16_step = lambda: ctx.gemm_bf16_f32(dAb, dBb, dCb, Mb, Mb, Mb)
-        settle(ctx, bf16_step, args.settle)
-        n_b = max(20, args.steps // 10)
-        ms_b = timed(ctx, timer, bf16_step, n_b, 5)
-        tf = 2.0 * Mb ** 3 / (ms_b * 1e-3) / 1e12
-        extras["gemm_bf16_8192"] = {"kernel": "gemm_bf16_pair", "ms_per_step": round(ms_b, 4),
-                                    "tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4),
-                                    "timed_launches": n_b, "warmup": 5,
-                                    "how": f"{args.settle} s of untimed launches, 5 warm-ups, then {n_b} back-to-back "
-                                           "launches between two events"}
-        for b in (dAb, dBb, dCb):
-            b.free()
-        # config 5: chained int8 MLP
-        Mm, Km, Fm, Nm = 2048, 4096, 11008, 4096
-        dXm, d1, d2 = ctx.empty((Mm, Km), np.int8), ctx.empty((Km, Fm), np.int8), ctx.empty((Fm, Nm), np.int8)
-        dH, dYm = ctx.empty((Mm, Fm), np.int8), ctx.empty((Mm, Nm), np.int8)
-        ctx.fill_i8(dXm, Mm * Km, 3)
-        ctx.fill_i8(d1, Km * Fm, 5)
-        ctx.fill_i8(d2, Fm * Nm, 6)
-        ms_m = timed(ctx, timer, lambda: ctx.mlp_i8(dXm, d1, d2, dH, dYm, Mm, Km, Fm, Nm, 11, 12),
-                     max(5, args.steps // 2), 2)
-        mops = 2.0 * 2 * Mm * Km * Fm
-        extras["mlp_i8"] = {"kernel": "gemm_i8_pipe2<256, 128, 4, NN, Y_HI_RELU> + gemm_i8_pipe2<256, 128, 4, NN, Y_HI>",
-                            "ms_per_step": round(ms_m, 4),
-                            "tops": round(mops / (ms_m * 1e-3) / 1e12, 1),
-                            "frac_of_peak": round(mops / (ms_m * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
-        for b in (dXm, d1, d2, dH, dYm):
-            b.free()
+        extras["conv2d_3x3"] = extra_conv(ctx, timer, args)
+        extras["gemm_i8_m_shard"] = extra_m_shard(ctx, timer, args)
+        extras["gemm_bf16_8192"] = extra_bf16(ctx, timer, args)
+        extras["mlp_i8"] = extra_mlp(ctx, timer, args)
     ctx.close()
     if not args.no_extras:
         extras["mfma_ceiling"] = mfma_ceiling()
