@@ -24,7 +24,10 @@ import numpy as np
 from . import synth  # noqa: F401  (re-exported)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libmiaie.so")
+# MIAIE_LIB_DIR selects another build of the same library (the host-sanitized
+# one in aiehlc_amd/lib_san, see aiehlc_amd/build.py); default aiehlc_amd/lib
+LIB_DIR = os.environ.get("MIAIE_LIB_DIR") or os.path.join(HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libmiaie.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "miaie.h")
 
 MIAIE_OK = 0

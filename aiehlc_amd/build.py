@@ -26,6 +26,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
+SANDIR = os.path.join(HERE, "lib_san")
 LIB = os.path.join(LIBDIR, "libmiaie.so")
 HARNESS = os.path.join(HERE, "harness")
 XAIE_SRC = os.path.join(CSRC, "xaie")
@@ -58,6 +59,22 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print("\n".join(lines), flush=True)
 
 
+# Host code of the libraries built again with AddressSanitizer and
+# UndefinedBehaviorSanitizer (device code is built as usual: the flags apply
+# to the host pass only).  The result, aiehlc_amd/lib_san/, is loaded by
+# setting MIAIE_LIB_DIR and preloading clang's ASan runtime (asan_runtime()).
+SAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-g"]
+
+
+def asan_runtime() -> str | None:
+    """clang's shared ASan runtime (the one hipcc's host pass instruments for)."""
+    import glob
+
+    hits = sorted(glob.glob("/opt/rocm/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    return hits[-1] if hits else None
+
+
 def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
@@ -79,7 +96,33 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     build_harness(verbose)
     build_hlc_samples(verbose)
     build_probes(verbose)
+    build_sanitized(verbose, jobs)
     return LIB
+
+
+def build_sanitized(verbose: bool = False, jobs: int | None = None) -> str:
+    """aiehlc_amd/lib_san/libmiaie.so and libmiaie_xaie.so with sanitized host code."""
+    sobj = os.path.join(OBJ, "san")
+    os.makedirs(sobj, exist_ok=True)
+    os.makedirs(SANDIR, exist_ok=True)
+    srcs = sources()
+    xsrcs = sorted(os.path.join(XAIE_SRC, f) for f in os.listdir(XAIE_SRC) if f.endswith(".hip"))
+    objs = [os.path.join(sobj, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    xobjs = [os.path.join(sobj, "xaie_" + os.path.basename(s)[:-4] + ".o") for s in xsrcs]
+    jobs = jobs or min(8, len(srcs) + len(xsrcs))
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, *SAN_FLAGS, "-c", s, "-o", o], verbose)
+                for s, o in zip(srcs + xsrcs, objs + xobjs)]
+        for f in futs:
+            f.result()
+    lib = os.path.join(SANDIR, "libmiaie.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", lib + ".tmp", *objs], verbose)
+    os.replace(lib + ".tmp", lib)
+    xlib = os.path.join(SANDIR, "libmiaie_xaie.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", xlib + ".tmp", *xobjs, f"-L{SANDIR}", "-lmiaie",
+          "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(xlib + ".tmp", xlib)
+    return lib
 
 
 def build_xaie(verbose: bool = False) -> str:

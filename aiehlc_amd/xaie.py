@@ -13,7 +13,10 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libmiaie_xaie.so")
+# MIAIE_LIB_DIR selects another build of the same library (the host-sanitized
+# one in aiehlc_amd/lib_san, see aiehlc_amd/build.py); default aiehlc_amd/lib
+LIB_DIR = os.environ.get("MIAIE_LIB_DIR") or os.path.join(HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libmiaie_xaie.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "miaie_xaie.h")
 
 XAIE_OK = 0

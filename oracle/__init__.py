@@ -24,7 +24,10 @@ _sz = C.c_size_t
 _u64 = C.c_uint64
 
 
-def _lib(name: str = "liboracle.so") -> C.CDLL:
+def _lib(name: str | None = None) -> C.CDLL:
+    # MIAIE_ORACLE_LIB selects another build of the same source (the
+    # sanitized liboracle_san.so)
+    name = name or os.environ.get("MIAIE_ORACLE_LIB") or "liboracle.so"
     if name in _LIBS:
         return _LIBS[name]
     path = os.path.join(_HERE, name)
@@ -119,7 +122,7 @@ def count_mismatch_i32(want: np.ndarray, got: np.ndarray) -> int:
 
 
 def gemm_i8(A: np.ndarray, B: np.ndarray, b_nt: bool = False, rows=None, nthreads=None,
-            lib: str = "liboracle.so") -> np.ndarray:
+            lib: str | None = None) -> np.ndarray:
     """int8 GEMM with int32 accumulation.  NT: oracle_gemm_i8_nt_rows; NN: oracle_gemm_i8_nn_rows.
 
     Returns C[row0:row1, :] (all rows by default)."""

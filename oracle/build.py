@@ -4,6 +4,8 @@ Compiles oracle/miaie_oracle.c with gcc into two shared libraries:
   oracle/liboracle.so     -O2 -fopenmp   (checker, and the timed CPU baseline)
   oracle/liboracle_os.so  -Os -fopenmp   (the reference host's -Os flag,
                                           script/aiehlc.sh:343, reported beside it)
+  oracle/liboracle_san.so -O1 -fopenmp with ASan and UBSan (the CPU tests run
+                                          under it, tests/test_sanitizers.py)
 
 The reference's own golden loops cannot be compiled here: they live inside
 harness programs that include aie-rt's xaiengine.h and the Xilinx BSP
@@ -19,6 +21,10 @@ SRC = os.path.join(HERE, "miaie_oracle.c")
 OUTS = {
     "liboracle.so": ["-O2"],
     "liboracle_os.so": ["-Os"],
+    # AddressSanitizer + UndefinedBehaviorSanitizer build, loaded by setting
+    # MIAIE_ORACLE_LIB=liboracle_san.so with gcc's libasan preloaded
+    "liboracle_san.so": ["-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                         "-fno-omit-frame-pointer"],
 }
 
 
