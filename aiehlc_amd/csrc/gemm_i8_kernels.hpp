@@ -1,0 +1,779 @@
+// int8 GEMM device code shared by the library (gemm_i8.hip) and the
+// in-kernel clock probe (probes/gemm_span.hip): the requantize epilogues and
+// the pipelined kernels gemm_i8_pipe and gemm_i8_pipe2.  The kernel list,
+// tiling and operand-role conventions are described at the top of
+// gemm_i8.hip.
+#pragma once
+
+#include <type_traits>
+
+#include "gfx950_ops.hpp"
+#include "miaie_internal.hpp"
+
+namespace miaie {
+namespace gemm {
+
+namespace dev = miaie::dev;
+
+
+// ------------------------------------------------------------- epilogue
+// y = sat_int8(floor((acc + 2^(s-1)) / 2^s)) for s in [1, 31], sat_int8(acc)
+// for s == 0; ReLU after the shift.  floor((a + 2^(s-1)) / 2^s) equals
+// (a >> s) + bit (s-1) of a, which cannot overflow.
+__device__ __forceinline__ int requant1(int acc, int s, int relu) {
+  int q = s ? (acc >> s) + ((acc >> (s - 1)) & 1) : acc;
+  q = relu ? max(q, 0) : q;
+  return min(max(q, -128), 127);
+}
+
+// The same requant in three instructions (add, arithmetic shift, med3) for
+// accumulators with |acc| + 2^(s-1) < 2^31, which holds for any int8 GEMM
+// with K < 2^16 (|acc| <= K * 2^14).  rnd = s ? 2^(s-1) : 0; lo = relu ? 0 : -128
+// (ReLU after the shift is the same as raising the lower clamp to 0).
+struct Requant {
+  int s, rnd, lo, hi;  // hi == 127, kept in a register (VOP3 takes no literal)
+  __device__ __forceinline__ int operator()(int acc) const {
+    int r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"((acc + rnd) >> s), "s"(lo), "v"(hi));
+    return r;
+  }
+  // four results packed little-endian into one dword (byte k = value k)
+  __device__ __forceinline__ uint32_t pack4(int a0, int a1, int a2, int a3) const {
+    const uint32_t lo2 = __builtin_amdgcn_perm((uint32_t)(*this)(a1), (uint32_t)(*this)(a0), 0x0c0c0400u);
+    const uint32_t hi2 = __builtin_amdgcn_perm((uint32_t)(*this)(a3), (uint32_t)(*this)(a2), 0x04000c0cu);
+    return lo2 | hi2;
+  }
+};
+
+// The same requant for s >= 8 in 7 instructions per 4 values.  With
+// u = (acc + rnd) >> (s - 8), floor division composes, so u >> 8 equals
+// (acc + rnd) >> s, and the high byte of sat_int16(u) is that value clamped
+// to [-128, 127]: in range it is u >> 8; above 32767 it is 127 = 32767 >> 8
+// (and u >> 8 >= 128); below -32768 it is -128 (and u >> 8 <= -129).
+// v_cvt_pk_i16_i32 saturates two such u into one dword, v_perm_b32 collects
+// the four high bytes.  ReLU clamps the int16 pairs at 0 first.
+typedef short miaie_v2s __attribute__((ext_vector_type(2)));
+template <bool RELU>
+struct RequantHi {
+  int sh, rnd;  // sh = s - 8 (s >= 8)
+  __device__ __forceinline__ uint32_t pair(int a, int b) const {
+    miaie_v2s p = __builtin_amdgcn_cvt_pk_i16((a + rnd) >> sh, (b + rnd) >> sh);
+    if constexpr (RELU) p = __builtin_elementwise_max(p, miaie_v2s{0, 0});
+    return __builtin_bit_cast(uint32_t, p);
+  }
+  __device__ __forceinline__ uint32_t pack4(int a0, int a1, int a2, int a3) const {
+    // bytes 1 and 3 of pair(a0, a1), then bytes 1 and 3 of pair(a2, a3)
+    return __builtin_amdgcn_perm(pair(a2, a3), pair(a0, a1), 0x07050301u);
+  }
+};
+
+// LDS tile rows are 64 bytes = four 16-byte chunks; chunk c of row r is
+// stored at chunk c ^ swz(r).  gfx950 serves a ds_read_b128 16 lanes at a
+// time from 64 four-byte banks; the MFMA fragment read has lanes 0..15 on
+// 16 consecutive rows at one logical chunk, and XOR with row bits 2-3 makes
+// those 16 reads cover all 64 banks (measured conflict-free with
+// SQ_LDS_BANK_CONFLICT; XOR with row bits 1-2 measured 2-way conflicts).
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * 64 + ((chunk ^ swz(row)) << 4); }
+
+// ---------------------------------------------------------- pipelined tile
+// Workgroup tile BM x BN (256x256, 256x128 or 128x128), k-step 64, four LDS
+// stages.  The stages are the AIE DMA ping-pong generalised to depth 4: tile
+// t+4 is copied global -> LDS (global_load_lds_dwordx4, no register staging)
+// while tiles t and t+1 are multiplied, half of it in each, so each copy has
+// over two tiles of MFMA work to land.
+// Each of the 4 waves owns a 128 x BN/2 quarter: 4 x (BN/64)
+// v_mfma_i32_32x32x32_i8 per 32-wide k-step, fragments double-buffered in
+// registers so the LDS reads of one k-step overlap the MFMAs of the other.
+// One barrier per tile.  BN = 128 halves the work per tile, for shapes whose
+// 256-wide tiles would leave CUs idle.
+//
+// LDS layouts (per stage):
+//   A  [256 rows][64 B]: 16-byte chunk c of row r at chunk c ^ swz(r).
+//   B NT [BN rows][64 B]: as A.
+//   B NN [64 k-rows][BN B] (row-major, as stored in memory): 16-byte chunk
+//      c of k-row k at chunk c ^ bswz(k).  MFMA fragments (16 consecutive k
+//      of one column per lane) are read with two ds_read_b64_tr_b8, which
+//      transpose 8x16 byte blocks on the fly; bswz spreads the 8 k-rows x 2
+//      column halves one 32-lane half reads over all banks.
+constexpr int BK = 64, STAGES = 4;
+
+// NW waves (4 or 8) tile the BM x BN workgroup tile as 2 x (NW/2): each
+// wave owns WM = BM/2 rows (NI = WM/32 A fragments) and WN = BN / (NW/2)
+// columns (NJ = WN/32 B fragments).
+template <int BM, int BN, int NW>
+struct PipeGeom {
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int WAVES_N = NW / 2;
+  static constexpr int WM = BM / 2;                    // rows per wave
+  static constexpr int WN = BN / WAVES_N;              // columns per wave
+  static constexpr int NI = WM / 32;                   // A fragments per wave per k-step
+  static constexpr int A_BYTES = BM * BK;             // 16 or 8 KiB
+  static constexpr int B_BYTES = BN * BK;             // 16 or 8 KiB
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+  static constexpr int CP_BYTES = 1024 * NW;          // one 16-byte copy by every thread
+  static constexpr int A_CP = A_BYTES / CP_BYTES;     // A copies per thread per tile
+  static constexpr int B_CP = B_BYTES / CP_BYTES;     // B copies per thread per tile
+  static constexpr int CP_PER_TILE = A_CP + B_CP;     // 16-byte LDS copies per thread per tile
+  static constexpr int NJ = WN / 32;                   // B fragments per wave per k-step
+  static constexpr int NMF = NI * NJ;                  // MFMAs per wave per k-step
+  static_assert(NI >= 1 && NJ >= 1 && A_CP >= 1 && B_CP >= 1, "tile too small for this many waves");
+  static_assert(BM * BN <= LDS_BYTES, "Y staging fits in the stages");
+};
+
+template <int BN>
+__device__ __forceinline__ int bswz(int k) {
+  return BN == 256 ? (k & 7) << 1 : ((k >> 1) & 3) << 1;
+}
+
+// Issue order of one k-step's LDS reads.  Reads are numbered as in
+// read_one (A fragment i -> i; NT B fragment j -> NI + j; NN B fragment j ->
+// NI + 2j and NI + 2j + 1, its two transposing halves), and go out in the
+// order the MFMA sequence (i, j) = (x / NJ, dev::snake_j<NJ>(x)) first needs
+// them: B0, A0, B1 .. B(NJ-1), A1 .. A(NI-1).  With reads issued RPS per MFMA slot
+// from the start of a phase, every fragment has landed several MFMAs before
+// the next phase consumes it, and the last read of a phase is far from the
+// wait that precedes the tile barrier.
+template <int NI, int NJ, bool B_NT>
+constexpr int read_order(int n) {
+  if (B_NT) {
+    if (n == 0) return NI;
+    if (n == 1) return 0;
+    if (n <= NJ) return NI + n - 1;
+    return n - NJ;
+  }
+  if (n < 2) return NI + n;
+  if (n == 2) return 0;
+  if (n <= 2 * NJ) return NI + n - 1;
+  return n - 2 * NJ;
+}
+constexpr int RPS = 2;  // LDS reads issued per MFMA slot
+
+// Requantized-output modes (the YQ template argument): no Y; the med3 form
+// for any shift; the int16-saturation form for shifts >= 8, without and with
+// ReLU.
+enum YMode { Y_NONE = 0, Y_MED3 = 1, Y_HI = 2, Y_HI_RELU = 3 };
+
+// Epilogue of the pipelined kernels.  acc[i][j][4g + t] holds row
+// m = wm*WM + 32i + lane%32, column n = wn*WN + 32j + 8g + 4*(lane/32) + t of
+// the BM x BN tile.  C (int32) is stored straight from the accumulators; Y is
+// requantized, staged in LDS (16-byte chunk index XOR row%16, within the row's
+// BN/16 chunks) and written with fully coalesced 16-byte stores.  Both stores
+// are non-temporal: nothing in the kernel reads them back, and lines left
+// dirty in L2 are written back when the kernel ends.  `lds` must be free (every
+// LDS read and copy of the main loop completed before its last barrier) and
+// hold BM * BN bytes; rnd_add is the rounding term still to be added.
+template <int BM, int BN, int NW, int YQ, bool WRITE_C, int NI, int NJ>
+__device__ __forceinline__ void pipe_epilogue(v16i (&acc)[NI][NJ], int8_t* lds, int tid, int wm, int wn, int fr,
+                                              int fh, int m0, int n0, int8_t* __restrict__ Y,
+                                              int32_t* __restrict__ C, int ldy, int ldc, int shift, int relu,
+                                              int rnd_add) {
+  constexpr int WM = BM / 2, WN = BN / (NW / 2), THREADS = 64 * NW;
+  if constexpr (WRITE_C) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int m = m0 + wm * WM + 32 * i + fr;
+          const int n = n0 + wn * WN + 32 * j + 8 * g + 4 * fh;
+          v4i v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(C + (size_t)m * ldc + n));
+        }
+  }
+  if constexpr (YQ != Y_NONE) {
+    // Y leaves in NI chunks of 64 rows (row block i of both wave rows, all BN
+    // columns), through two LDS buffers: chunk i is requantized into buffer
+    // i % 2, then, after a barrier, written with coalesced 16-byte stores
+    // while the waves go on to requantize chunk i + 1.  Every workgroup of a
+    // launch reaches its epilogue at about the same time, so the stores of
+    // one chunk drain while the next chunk's VALU work (accumulator reads,
+    // shifts, saturating packs) runs, instead of after all of it.  Buffer
+    // i % 2 is rewritten for chunk i + 2 only after the barrier of chunk
+    // i + 1, which every wave reaches after its own loads of chunk i.
+    constexpr int CH = BN / 16;  // 16-byte chunks per row
+    constexpr int CR = 64;       // rows per chunk
+    constexpr int CB = CR * BN;  // bytes per chunk buffer
+    static_assert(2 * CB <= BM * BN && (CR * CH) % THREADS == 0, "two chunk buffers fit the stages");
+    auto stage_rows = [&](const auto& rq, int i, int8_t* buf) {
+      const int ml = 32 * wm + fr;  // row within the chunk
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = wn * WN + 32 * j + 8 * g + 4 * fh;
+          const uint32_t packed = rq.pack4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                           acc[i][j][4 * g + 3]);
+          const int off = ml * BN + ((((n >> 4) ^ (ml & (CH - 1)))) << 4) + (n & 15);
+          *reinterpret_cast<uint32_t*>(buf + off) = packed;
+        }
+    };
+    auto store_rows = [&](int i, const int8_t* buf) {
+#pragma unroll
+      for (int it = 0; it < CR * CH / THREADS; ++it) {
+        const int flat = it * THREADS + tid;
+        const int ml = flat / CH, c = flat % CH;
+        const int m = (ml / 32) * WM + 32 * i + (ml % 32);  // row within the tile
+        const v4i v = *reinterpret_cast<const v4i*>(buf + ml * BN + ((c ^ (ml & (CH - 1))) << 4));
+        __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + c * 16));
+      }
+    };
+    auto run = [&](const auto& rq) {
+      __syncthreads();  // the main loop's last LDS reads are done
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        int8_t* const buf = lds + (i & 1) * CB;
+        stage_rows(rq, i, buf);
+        __syncthreads();
+        store_rows(i, buf);
+      }
+    };
+    if constexpr (YQ == Y_HI_RELU)
+      run(RequantHi<true>{shift - 8, rnd_add});
+    else if constexpr (YQ == Y_HI)
+      run(RequantHi<false>{shift - 8, rnd_add});
+    else
+      run(Requant{shift, rnd_add, relu ? 0 : -128, 127});
+  }
+}
+
+template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
+    int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
+    int relu) {
+  using G = PipeGeom<BM, BN, NW>;
+  constexpr bool WRITE_Y = YQ != Y_NONE;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS_BYTES];
+  const uint32_t lds0 = dev::lds_addr(lds);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  int tm, tn;
+  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KT = K / BK;
+
+  // ---- LDS copy assignment.  Copy i of wave w fills the 1 KiB block NW*i + w
+  // of an operand's stage region:
+  //   A (and NT B): rows 16*(NW*i + w) + lane/4, physical chunk lane%4;
+  //   NN B: k-rows (NW*i + w) * (1024 / BN) + lane / (BN / 16), physical
+  //   chunk lane % (BN / 16).
+  const int a_r = 16 * wave + (lane >> 2);
+  const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 3) ^ swz(a_r));  // swz(a_r + 16*NW*i) == swz(a_r)
+  const int8_t* const a_base = A + (size_t)m0 * lda;
+  uint32_t b_voff;
+  const int8_t* b_base;
+  constexpr int B_ROWS_PER_CP = B_NT ? 16 * NW : 1024 * NW / BN;  // operand rows between copies i and i+1
+  if constexpr (B_NT) {
+    b_voff = (uint32_t)a_r * ldb + 16 * ((lane & 3) ^ swz(a_r));
+    b_base = B + (size_t)n0 * ldb;
+  } else {
+    constexpr int CPR = BN / 16;  // 16-byte chunks per k-row
+    const int b_r = (1024 / BN) * wave + lane / CPR;  // bswz(b_r + B_ROWS_PER_CP * i) == bswz(b_r)
+    b_voff = (uint32_t)b_r * ldb + 16 * ((lane % CPR) ^ bswz<BN>(b_r));
+    b_base = B + n0;
+  }
+
+  // copy x (< CP_PER_TILE) of tile kt into stage `stage`
+  auto copy = [&](int kt, int stage, int x) {
+    const uint32_t st = lds0 + stage * G::STAGE_BYTES + 1024 * wave;
+    if (x < G::A_CP) {
+      dev::gload_lds16(a_base + (size_t)kt * BK + (size_t)(16 * NW * x) * lda, a_voff, st + G::CP_BYTES * x);
+    } else {
+      const int i = x - G::A_CP;
+      const int8_t* bb = B_NT ? b_base + (size_t)kt * BK : b_base + (size_t)kt * BK * ldb;
+      dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * i) * ldb, b_voff, st + G::A_BYTES + G::CP_BYTES * i);
+    }
+  };
+
+  // ---- fragment offsets within a stage.
+  // A fragment (ks, i): row wm*128 + 32i + lane%32, logical chunk 2ks + lane/32.
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+  const int fr = lane & 31, fh = lane >> 5;
+  int a_fo[2], b_fo[G::NJ > 2 ? G::NJ : 2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) a_fo[ks] = (wm * G::WM + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+  if constexpr (B_NT) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      b_fo[ks] = G::A_BYTES + (wn * G::WN + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+  } else {
+    // tr8 read (ks, j, r): lane 16g + 2jj + h supplies k-row 32ks + 16(g>>1) + 8r + jj,
+    // columns wn*WN + 32j + 16(g&1) + 8h .. +8; it receives column
+    // wn*WN + 32j + lane%32, k = 32ks + 16*(lane/32) + 8r + (0..7).
+    // bswz of those k-rows depends on jj only.
+    const int g = lane >> 4, jj = (lane >> 1) & 7, h = lane & 1;
+#pragma unroll
+    for (int j = 0; j < G::NJ; ++j) {
+      const int c = wn * (G::WN / 16) + 2 * j + (g & 1);
+      b_fo[j] = G::A_BYTES + (16 * (g >> 1) + jj) * BN + ((c ^ bswz<BN>(jj)) << 4) + 8 * h;
+    }
+  }
+
+  // One k-step's fragments: NI A fragments, and NJ B fragments (NT: one
+  // ds_read_b128 each; NN: two tr8 halves each).
+  struct Frags {
+    v4i a[G::NI];
+    v4i b[G::NJ];                  // NT
+    miaie_v2i lo[G::NJ], hi[G::NJ];  // NN
+  };
+  constexpr int NREAD = G::NI + (B_NT ? 1 : 2) * G::NJ;  // LDS read instructions per k-step
+  // q-th LDS read of k-step ks of `stage` into f
+  auto read_one = [&](int stage, int ks, int q, Frags& f) {
+    const int8_t* s = lds + stage * G::STAGE_BYTES;
+    if (q < G::NI) {
+      f.a[q] = *reinterpret_cast<const v4i*>(s + a_fo[ks] + 2048 * q);
+    } else if constexpr (B_NT) {
+      f.b[q - G::NI] = *reinterpret_cast<const v4i*>(s + b_fo[ks] + 2048 * (q - G::NI));
+    } else {
+      const int j = (q - G::NI) >> 1;
+      if (((q - G::NI) & 1) == 0)
+        f.lo[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN);
+      else
+        f.hi[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN + 8 * BN);
+    }
+  };
+  auto bfrag = [&](const Frags& f, int j) -> v4i {
+    if constexpr (B_NT)
+      return f.b[j];
+    else
+      return v4i{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
+  };
+
+  // When only the requantized output is wanted, the accumulators start at
+  // the rounding term 2^(shift-1) so the epilogue needs no add.
+  const int rnd = shift ? 1 << (shift - 1) : 0;
+  const int acc0 = (WRITE_Y && !WRITE_C) ? rnd : 0;
+  v16i acc[G::NI][G::NJ];
+#pragma unroll
+  for (int i = 0; i < G::NI; ++i)
+#pragma unroll
+    for (int j = 0; j < G::NJ; ++j)
+      acc[i][j] = v16i{acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0};
+
+  constexpr int CP = G::CP_PER_TILE;
+  // A tile's CP copies go out in two halves, each spread evenly over the
+  // MFMA slots of one phase: the first CP_A in phase 2 of the tile four
+  // earlier (right after the barrier that frees their stage), the other CP_B
+  // in phase 1 of the tile three earlier.  Issuing a whole tile's copies in
+  // one phase saturates the vector-memory path (each copy moves 1 KiB), and
+  // the in-order wave then stalls its MFMAs behind them.
+  constexpr int CP_A = (CP + 1) / 2, CP_B = CP - CP_A;
+
+  // ---- prologue: tiles 0..2 and the first half of tile 3 in flight (tile
+  // 0's phase 1 sends the second half), wait for tile 0
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+    if (s < KT) {
+#pragma unroll
+      for (int x = 0; x < (s == STAGES - 1 ? CP_A : CP); ++x) copy(s, s, x);
+    }
+  if (KT >= 4)
+    dev::wait_vmcnt<2 * CP + CP_A>();
+  else if (KT == 3)
+    dev::wait_vmcnt<2 * CP>();
+  else if (KT == 2)
+    dev::wait_vmcnt<CP>();
+  else
+    dev::wait_vmcnt<0>();
+  dev::barrier();
+
+  Frags f0, f1;
+#pragma unroll
+  for (int n = 0; n < NREAD; ++n) read_one(0, 0, read_order<G::NI, G::NJ, B_NT>(n), f0);
+
+  // reads of slot x of a phase (RPS per slot, in read_order)
+  auto read_slot = [&](int stage, int ks, int x, Frags& f) {
+#pragma unroll
+    for (int r = 0; r < RPS; ++r)
+      if (RPS * x + r < NREAD) read_one(stage, ks, read_order<G::NI, G::NJ, B_NT>(RPS * x + r), f);
+  };
+  constexpr int READ_SLOTS = (NREAD + RPS - 1) / RPS;
+
+  auto copy_slot = [&](int kt_dst, int stage, int x, int first, int count) {
+#pragma unroll
+    for (int c = 0; c < count; ++c)
+      if ((c * G::NMF) / count == x) copy(kt_dst, stage, first + c);
+  };
+
+  // Per tile: phase 1 multiplies k-step 0 (f0) while the reads of k-step 1
+  // (f1) and the second half of tile kt+3's copies go out between the MFMAs;
+  // then the tile barrier; phase 2 multiplies k-step 1 while the first half
+  // of tile kt+4's copies and the k-step-0 reads of tile kt+1 go out between
+  // the MFMAs.  sched_fence() pins this interleave.
+  // PRE: tile kt+3 exists (its first half went out in phase 2 of tile kt-1,
+  // or in the prologue for tile 3); MORE: tile kt+4 exists; NEXT: tile kt+1
+  // exists; VM: copies still allowed in flight once tile kt+1 has landed
+  // (those of tiles kt+2 and kt+3, the last ones issued).
+  auto tile = [&](int kt, auto pre_c, auto more_c, auto next_c, auto vm_c) {
+    constexpr bool PRE = decltype(pre_c)::value, MORE = decltype(more_c)::value;
+    constexpr bool NEXT = decltype(next_c)::value;
+    constexpr int VM = decltype(vm_c)::value;
+    const int cur = kt & (STAGES - 1);
+    // stage of tile kt+3 = stage of tile kt-1, whose last reads completed
+    // before tile kt-1's barrier (for kt = 0: stage 3, not read yet)
+    const int pre_stage = (kt + 3) & (STAGES - 1);
+#pragma unroll
+    for (int x = 0; x < G::NMF; ++x) {
+      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
+      read_slot(cur, 1, x, f1);
+      if constexpr (PRE) copy_slot(kt + 3, pre_stage, x, CP_A, CP_B);
+      dev::sched_fence();
+    }
+    if constexpr (READ_SLOTS > G::NMF) {
+#pragma unroll
+      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(cur, 1, x, f1);
+    }
+    // Tile kt+1 must have landed (own copies, then everyone's via the
+    // barrier); after the barrier no wave reads stage `cur` again, so the
+    // copies of tile kt+4 may overwrite it.
+    dev::waitcnt<VM, 0>();
+    dev::barrier();
+    const int nxt = (kt + 1) & (STAGES - 1);
+#pragma unroll
+    for (int x = 0; x < G::NMF; ++x) {
+      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
+      if constexpr (MORE) copy_slot(kt + STAGES, cur, x, 0, CP_A);
+      if constexpr (NEXT) read_slot(nxt, 0, x, f0);
+      dev::sched_fence();
+    }
+    if constexpr (NEXT && READ_SLOTS > G::NMF) {
+#pragma unroll
+      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(nxt, 0, x, f0);
+    }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using V2 = std::integral_constant<int, 2 * CP>;
+  using V1 = std::integral_constant<int, CP>;
+  using V0 = std::integral_constant<int, 0>;
+  int kt = 0;
+  for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, T_{}, V2{});
+  if (kt == KT - 4) tile(kt++, T_{}, F_{}, T_{}, V2{});
+  if (kt == KT - 3) tile(kt++, F_{}, F_{}, T_{}, V1{});
+  if (kt == KT - 2) tile(kt++, F_{}, F_{}, T_{}, V0{});
+  tile(kt, F_{}, F_{}, F_{}, V0{});
+
+  pipe_epilogue<BM, BN, NW, YQ, WRITE_C>(acc, lds, tid, wm, wn, fr, fh, m0, n0, Y, C, ldy, ldc, shift, relu,
+                                        rnd - acc0);
+}
+
+// ------------------------------------------------------ pair-staged tile
+// gemm_i8_pipe with A staged two k-tiles at a time.  A row-major A tile
+// row contributes 64 bytes per k-tile, so a per-k-tile copy touches every
+// 128-byte line at half use; the L1 fetches whole lines, the address path
+// handles 16 lines per 1 KiB copy, and the A stream costs twice its bytes on
+// the L2 -> L1 path.  Here A lives in NA2 = 3 pair stages of BM rows x 128
+// bytes (k-tiles 2p and 2p+1 of pair p in stage p % 3) and each 1 KiB copy
+// moves 8 whole lines; B keeps its four per-k-tile stages.  Needs K % 128 == 0.
+//
+// Copy schedule, in phases phi = 2t + (h - 1) (tile t, phase h = 1, 2):
+//   B tile k: first half at phi = 2k - 7 (phase 2 of tile k-4, after the
+//     barrier that retires tile k-4's reads of its stage), second half at
+//     phi = 2k - 6 (phase 1 of tile k-3);
+//   A pair p: quarter q at phi = 4p - 9 + q (phase 2 of tile 2p-5, after the
+//     barrier that retires pair p-3's reads of its stage, through phase 1 of
+//     tile 2p-3).
+// Copies with phi < 0 go out in the prologue, in phi order.  Tile t's data
+// (B tile t, A pair t/2) was issued by phase 2t - 6, so the barrier of tile
+// t-1 (end of phase 2t - 2) waits until at most the copies of the four phases
+// after it are in flight: 2 * (copies per tile) in steady state, fewer in the
+// last tiles (dev::pair_vm).
+constexpr int NA2 = 3;
+
+template <int BM, int BN, int NW>
+struct Pipe2Geom {
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int WAVES_N = NW / 2;
+  static constexpr int WM = BM / 2, WN = BN / WAVES_N;
+  static constexpr int NI = WM / 32, NJ = WN / 32, NMF = NI * NJ;
+  static constexpr int A2_BYTES = BM * 128;                 // one A pair stage
+  static constexpr int A_REGION = NA2 * A2_BYTES;
+  static constexpr int B_BYTES = BN * BK;                   // one B stage
+  static constexpr int LDS_BYTES = A_REGION + STAGES * B_BYTES;
+  static constexpr int CP_BYTES = 1024 * NW;                // one 16-byte copy by every thread
+  static constexpr int A_CP2 = A2_BYTES / CP_BYTES;         // A copies per thread per pair
+  static constexpr int QA = A_CP2 / 4;                      // ... per quarter (per phase)
+  static constexpr int B_CP = B_BYTES / CP_BYTES;           // B copies per thread per k-tile
+  static constexpr int B_CP0 = (B_CP + 1) / 2, B_CP1 = B_CP - B_CP0;
+  static constexpr int CP = A_CP2 / 2 + B_CP;               // copies per thread per k-tile
+  static_assert(NI >= 1 && NJ >= 1 && B_CP >= 1 && A_CP2 % 4 == 0 && QA >= 1, "pair-staged geometry");
+  static_assert(LDS_BYTES <= 163840 && BM * BN <= LDS_BYTES, "pair-staged LDS budget");
+};
+
+// Clock probe records per wave (TIMED instantiations only): shader clock at
+// the start, after the prologue's barrier, after the last k-tile and at the
+// end, then the 100 MHz wall clock at the start and the end.
+constexpr int PROBE_WORDS = 6;
+
+template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED = false>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
+    int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
+    int relu, unsigned long long* __restrict__ probe) {
+  unsigned long long t0 = 0, r0 = 0, t1 = 0, t2 = 0;
+  if constexpr (TIMED) {
+    t0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  using G = Pipe2Geom<BM, BN, NW>;
+  constexpr bool WRITE_Y = YQ != Y_NONE;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS_BYTES];
+  const uint32_t lds0 = dev::lds_addr(lds);
+  int8_t* const bl = lds + G::A_REGION;  // B stages
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  int tm, tn;
+  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KT = K / BK;  // even
+
+  // ---- copy assignment.  A copy x of wave w fills the 1 KiB block NW*x + w
+  // of a pair stage: rows 8*(NW*x + w) + lane/8, physical chunk lane%8 of the
+  // row's 128 bytes, holding logical chunk (lane%8) ^ aswz(row) with
+  // aswz(row) = (row >> 1) & 7 (= 4*(w&1) + lane/16 for every x).  The MFMA
+  // fragment read (16 consecutive rows at one logical chunk) then touches 16
+  // distinct 16-byte bank groups.  B copies as in gemm_i8_pipe.
+  const int a_r = 8 * wave + (lane >> 3);
+  const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 7) ^ ((a_r >> 1) & 7));
+  const int8_t* const a_base = A + (size_t)m0 * lda;
+  uint32_t b_voff;
+  const int8_t* b_base;
+  constexpr int B_ROWS_PER_CP = B_NT ? 16 * NW : 1024 * NW / BN;
+  if constexpr (B_NT) {
+    const int b_r = 16 * wave + (lane >> 2);
+    b_voff = (uint32_t)b_r * ldb + 16 * ((lane & 3) ^ swz(b_r));
+    b_base = B + (size_t)n0 * ldb;
+  } else {
+    constexpr int CPR = BN / 16;
+    const int b_r = (1024 / BN) * wave + lane / CPR;
+    b_voff = (uint32_t)b_r * ldb + 16 * ((lane % CPR) ^ bswz<BN>(b_r));
+    b_base = B + n0;
+  }
+  // copy x (< A_CP2) of A pair p; copy x (< B_CP) of B k-tile kt
+  auto copy_a = [&](int p, int x) {
+    const uint32_t st = lds0 + (p % NA2) * G::A2_BYTES + 1024 * wave + G::CP_BYTES * x;
+    dev::gload_lds16(a_base + (size_t)p * 128 + (size_t)(8 * NW * x) * lda, a_voff, st);
+  };
+  auto copy_b = [&](int kt, int x) {
+    const uint32_t st = lds0 + G::A_REGION + (kt & (STAGES - 1)) * G::B_BYTES + 1024 * wave + G::CP_BYTES * x;
+    const int8_t* bb = B_NT ? b_base + (size_t)kt * BK : b_base + (size_t)kt * BK * ldb;
+    dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * x) * ldb, b_voff, st);
+  };
+
+  // ---- fragment offsets.  A fragment (par, ks, i) of k-tile 2p + par: row
+  // wm*WM + 32i + lane%32 of pair stage p % 3, logical chunk 4par + 2ks +
+  // lane/32, physical chunk XOR (row >> 1) & 7 = (lane%32 >> 1) & 7.
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+  const int fr = lane & 31, fh = lane >> 5;
+  int a_fo[2][2], b_fo[G::NJ > 2 ? G::NJ : 2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      a_fo[par][ks] = (wm * G::WM + fr) * 128 + (((4 * par + 2 * ks + fh) ^ ((fr >> 1) & 7)) << 4);
+  if constexpr (B_NT) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) b_fo[ks] = (wn * G::WN + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+  } else {
+    // tr8 halves as in gemm_i8_pipe
+    const int g = lane >> 4, jj = (lane >> 1) & 7, h = lane & 1;
+#pragma unroll
+    for (int j = 0; j < G::NJ; ++j) {
+      const int c = wn * (G::WN / 16) + 2 * j + (g & 1);
+      b_fo[j] = (16 * (g >> 1) + jj) * BN + ((c ^ bswz<BN>(jj)) << 4) + 8 * h;
+    }
+  }
+
+  struct Frags {
+    v4i a[G::NI];
+    v4i b[G::NJ];
+    miaie_v2i lo[G::NJ], hi[G::NJ];
+  };
+  constexpr int NREAD = G::NI + (B_NT ? 1 : 2) * G::NJ;
+  // q-th LDS read of k-step ks of k-tile kt (parity PAR) into f
+  auto read_one = [&](int kt, auto par_c, int ks, int q, Frags& f) {
+    constexpr int PAR = decltype(par_c)::value;
+    if (q < G::NI) {
+      const int8_t* s = lds + ((kt >> 1) % NA2) * G::A2_BYTES;
+      f.a[q] = *reinterpret_cast<const v4i*>(s + a_fo[PAR][ks] + 4096 * q);
+    } else {
+      const int8_t* s = bl + (kt & (STAGES - 1)) * G::B_BYTES;
+      if constexpr (B_NT) {
+        f.b[q - G::NI] = *reinterpret_cast<const v4i*>(s + b_fo[ks] + 2048 * (q - G::NI));
+      } else {
+        const int j = (q - G::NI) >> 1;
+        if (((q - G::NI) & 1) == 0)
+          f.lo[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN);
+        else
+          f.hi[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN + 8 * BN);
+      }
+    }
+  };
+  auto bfrag = [&](const Frags& f, int j) -> v4i {
+    if constexpr (B_NT)
+      return f.b[j];
+    else
+      return v4i{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
+  };
+  // LDS reads per MFMA slot: one at 256x256 (16 slots for 12 reads; 1152
+  // against 1190 cycles per k-tile with two), two at 256x128 (8 slots for 8
+  // reads; 655 against 669 with one)
+  constexpr int RPS2 = G::NMF >= 16 ? 1 : 2;
+  constexpr int READ_SLOTS = (NREAD + RPS2 - 1) / RPS2;
+  auto read_slot = [&](int kt, auto par_c, int ks, int x, Frags& f) {
+#pragma unroll
+    for (int r = 0; r < RPS2; ++r)
+      if (RPS2 * x + r < NREAD) read_one(kt, par_c, ks, read_order<G::NI, G::NJ, B_NT>(RPS2 * x + r), f);
+  };
+
+  const int rnd = shift ? 1 << (shift - 1) : 0;
+  const int acc0 = (WRITE_Y && !WRITE_C) ? rnd : 0;
+  v16i acc[G::NI][G::NJ];
+#pragma unroll
+  for (int i = 0; i < G::NI; ++i)
+#pragma unroll
+    for (int j = 0; j < G::NJ; ++j)
+      acc[i][j] = v16i{acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0};
+
+  // ---- prologue: phases -9 .. -1 in order (B tiles 0..2, the first half of
+  // B tile 3, A pairs 0 and 1, the first quarter of A pair 2), then wait for
+  // B tile 0 and A pair 0 (issued by phase -6).
+  const int KP = KT / 2;
+#pragma unroll
+  for (int phi = -9; phi < 0; ++phi) {
+    if ((phi & 1) != 0) {
+      const int k = (phi + 7) / 2;  // B first half
+      if (phi >= -7 && k < KT)
+#pragma unroll
+        for (int x = 0; x < G::B_CP0; ++x) copy_b(k, x);
+    } else {
+      const int k = (phi + 6) / 2;  // B second half
+      if (phi >= -6 && k < KT)
+#pragma unroll
+        for (int x = G::B_CP0; x < G::B_CP; ++x) copy_b(k, x);
+    }
+    const int p = (phi + 9) / 4, q = (phi + 9) % 4;
+    if (p < KP)
+#pragma unroll
+      for (int x = 0; x < G::QA; ++x) copy_a(p, G::QA * q + x);
+  }
+  if (KT >= 6)
+    dev::wait_vmcnt<dev::pair_prologue_vm(G::B_CP0, G::B_CP1, G::QA)>();
+  else
+    dev::wait_vmcnt<0>();
+  dev::barrier();
+  if constexpr (TIMED) t1 = __builtin_amdgcn_s_memtime();
+
+  Frags f0, f1;
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+#pragma unroll
+  for (int n = 0; n < NREAD; ++n) read_one(0, P0{}, 0, read_order<G::NI, G::NJ, B_NT>(n), f0);
+
+  // The copies of one phase: nb B copies (first_b ..) of k-tile kb and na A
+  // copies (first_a ..) of pair pa, spread evenly over the MFMA slots.
+  auto copy_slot = [&](int x, int kb, int first_b, int nb, int pa, int first_a, int na) {
+#pragma unroll
+    for (int c = 0; c < nb + na; ++c)
+      if ((c * G::NMF) / (nb + na) == x) {
+        if (c < nb)
+          copy_b(kb, first_b + c);
+        else
+          copy_a(pa, first_a + c - nb);
+      }
+  };
+
+  // Tile t (parity PAR, D tiles before the last; D >= 6 for every tile of the
+  // steady loop): phase 1 multiplies k-step 0 while the k-step-1 reads and
+  // the phase's copies go out; barrier; phase 2 multiplies k-step 1 while the
+  // phase's copies and tile t+1's k-step-0 reads go out.
+  auto tile = [&](int t, auto par_c, auto d_c) {
+    constexpr int PAR = decltype(par_c)::value, D = decltype(d_c)::value;
+    constexpr int NB1 = D >= 3 ? G::B_CP1 : 0, NB2 = D >= 4 ? G::B_CP0 : 0;
+    constexpr int NA1 = (PAR == 0 ? D >= 5 : D >= 4) ? G::QA : 0;
+    constexpr int NA2_ = (PAR == 0 ? D >= 5 : D >= 6) ? G::QA : 0;
+    constexpr bool NEXT = D >= 1;
+    constexpr int VM = dev::pair_vm(D, G::B_CP0, G::B_CP1, G::QA);
+    // phase 1: B k-tile t+3 (second half); A pair t/2+2 quarter 1 (t even) or
+    // pair (t+3)/2 quarter 3 (t odd)
+    const int pa1 = PAR == 0 ? (t >> 1) + 2 : (t + 3) >> 1;
+    constexpr int qa1 = PAR == 0 ? 1 : 3;
+#pragma unroll
+    for (int x = 0; x < G::NMF; ++x) {
+      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
+      read_slot(t, par_c, 1, x, f1);
+      copy_slot(x, t + 3, G::B_CP0, NB1, pa1, G::QA * qa1, NA1);
+      dev::sched_fence();
+    }
+    if constexpr (READ_SLOTS > G::NMF) {
+#pragma unroll
+      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(t, par_c, 1, x, f1);
+    }
+    // next k-tile's data has landed (own copies, then everyone's via the
+    // barrier); after the barrier no wave reads this tile's B stage again
+    dev::waitcnt<VM, 0>();
+    dev::barrier();
+    // phase 2: B k-tile t+4 (first half); A pair t/2+2 quarter 2 (t even) or
+    // pair (t+5)/2 quarter 0 (t odd)
+    const int pa2 = PAR == 0 ? (t >> 1) + 2 : (t + 5) >> 1;
+    constexpr int qa2 = PAR == 0 ? 2 : 0;
+    using PN = std::integral_constant<int, 1 - PAR>;
+#pragma unroll
+    for (int x = 0; x < G::NMF; ++x) {
+      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
+      copy_slot(x, t + 4, 0, NB2, pa2, G::QA * qa2, NA2_);
+      if constexpr (NEXT) read_slot(t + 1, PN{}, 0, x, f0);
+      dev::sched_fence();
+    }
+    if constexpr (NEXT && READ_SLOTS > G::NMF) {
+#pragma unroll
+      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(t + 1, PN{}, 0, x, f0);
+    }
+  };
+  using DS = std::integral_constant<int, 64>;  // steady state
+  int t = 0;
+  for (; t + 6 < KT; t += 2) {
+    tile(t, P0{}, DS{});
+    tile(t + 1, P1{}, DS{});
+  }
+  if (KT >= 6) {
+    tile(t, P0{}, std::integral_constant<int, 5>{});
+    tile(t + 1, P1{}, std::integral_constant<int, 4>{});
+    t += 2;
+  }
+  if (KT >= 4) {
+    tile(t, P0{}, std::integral_constant<int, 3>{});
+    tile(t + 1, P1{}, std::integral_constant<int, 2>{});
+    t += 2;
+  }
+  tile(t, P0{}, std::integral_constant<int, 1>{});
+  tile(t + 1, P1{}, std::integral_constant<int, 0>{});
+  if constexpr (TIMED) t2 = __builtin_amdgcn_s_memtime();
+
+  pipe_epilogue<BM, BN, NW, YQ, WRITE_C>(acc, lds, tid, wm, wn, fr, fh, m0, n0, Y, C, ldy, ldc, shift, relu,
+                                        rnd - acc0);
+  if constexpr (TIMED) {
+    const unsigned long long t3 = __builtin_amdgcn_s_memtime(), r3 = __builtin_amdgcn_s_memrealtime();
+    const unsigned long long rec[PROBE_WORDS] = {t0, t1, t2, t3, r0, r3};
+    unsigned long long v = 0;
+#pragma unroll
+    for (int i = 0; i < PROBE_WORDS; ++i) v = lane == i ? rec[i] : v;
+    if (lane < PROBE_WORDS) probe[((size_t)blockIdx.x * NW + wave) * PROBE_WORDS + lane] = v;
+  }
+}
+
+}  // namespace gemm
+}  // namespace miaie

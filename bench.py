@@ -15,6 +15,9 @@ Also in the line (not the headline):
                          sharded over M, with the tile the planner picks
   extras.mfma_ceiling    register-only MFMA rate on this GPU, constant and
                          random operands (aiehlc_amd/probes/mfma_ceiling)
+  extras.gemm_in_kernel  the headline kernel's in-kernel clocks (prologue,
+                         cycles per k-tile, epilogue, workgroup end spread,
+                         clock per XCD; aiehlc_amd/probes/gemm_span)
   extras.launch_floor    time per back-to-back launch of an empty kernel with the
                          conv's and the GEMM's grid and LDS size
                          (aiehlc_amd/probes/launch_floor); the conv line carries
@@ -58,6 +61,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_rq_4096_traffic.txt")
 CEILING_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "mfma_ceiling")
 FLOOR_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "launch_floor")
 CONV_SPAN_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "conv_span")
+GEMM_SPAN_EXE = os.path.join(ROOT, "aiehlc_amd", "probes", "gemm_span")
 FLOWS_EXE = os.path.join(ROOT, "aiehlc_amd", "harness", "xaie_flows")
 METRIC = "int8 GEMM TOPS (% MFMA peak) at 4096^3; int8 conv2d 3x3 GOPS; vs host CPU"
 
@@ -547,6 +551,10 @@ def main() -> int:
     ctx.close()
     if not args.no_extras:
         extras["mfma_ceiling"] = mfma_ceiling()
+        # the headline kernel's in-kernel clocks: prologue / k-tile / epilogue
+        # cycles, workgroup start and end spread, per-XCD clock
+        # (aiehlc_amd/probes/gemm_span, the same kernel template with clock records)
+        extras["gemm_in_kernel"] = probe_json(GEMM_SPAN_EXE)
         extras["reference_flow_16x16"] = reference_flow()
         extras["reference_flow_8x8"] = reference_flow("mm8", 8, 15.0)
         floor = probe_json(FLOOR_EXE)
@@ -561,7 +569,7 @@ def main() -> int:
 
     roofline = {
         "bound": "mfma",
-        "kernel": "gemm_i8_pipe2<256, 256, 4, NN, Y_HI> (rocprof: gemm_i8_pipe2<256, 256, 4, false, 2, false>)",
+        "kernel": "gemm_i8_pipe2<256, 256, 4, NN, Y_HI> (rocprof: miaie::gemm::gemm_i8_pipe2<256, 256, 4, false, 2, false, false>)",
         "achieved": round(tops, 2),
         "peak": PEAK_INT8_TOPS,
         "unit": "TFLOP/s",
