@@ -156,6 +156,7 @@ def _addr(x) -> int | None:
 
 KERNEL_TILE64 = 0
 KERNEL_PIPE = 1
+KERNEL_PIPE_MIXED = 2  # 256x256 tiles, then 256x128 tiles over the last columns
 
 
 class GemmPlan(C.Structure):

@@ -251,13 +251,39 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
   }
 }
 
+template <bool B_NT>
+void launch_pipe_mixed(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
+                       int lda, int ldb, int ldy, int ldc, int shift, int relu, int nw) {
+  const dim3 grid((M / 256) * (nw + (N - 256 * nw) / 128)), block(256);
+  const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw);
+  };
+  if (C) {
+    switch (yq) {
+      case Y_NONE: go(gemm_i8_pipe2_mixed<B_NT, Y_NONE, true>); break;
+      case Y_MED3: go(gemm_i8_pipe2_mixed<B_NT, Y_MED3, true>); break;
+      case Y_HI: go(gemm_i8_pipe2_mixed<B_NT, Y_HI, true>); break;
+      default: go(gemm_i8_pipe2_mixed<B_NT, Y_HI_RELU, true>); break;
+    }
+  } else {
+    switch (yq) {
+      case Y_MED3: go(gemm_i8_pipe2_mixed<B_NT, Y_MED3, false>); break;
+      case Y_HI: go(gemm_i8_pipe2_mixed<B_NT, Y_HI, false>); break;
+      default: go(gemm_i8_pipe2_mixed<B_NT, Y_HI_RELU, false>); break;
+    }
+  }
+}
+
 // Tiling planner for the pipelined kernel: picks the workgroup tile
 // (BM x BN) among 256x256, 256x128 and 128x128 for an M x N x K product on
-// `cus` compute units.  Cost, in units of one 256x256x64 k-tile of MFMA
-// work: the rounds of one workgroup per CU times one workgroup's work, its
-// K/64 k-tiles plus about 6 units of prologue and epilogue, scaled by the
-// tile's relative cost per k-tile (1 for 256x256; 0.55 for 256x128; 0.35
-// for 128x128, whose LDS reads per MFMA are twice those of 256x256).
+// `cus` compute units, or a mix of 256x256 and 256x128 tiles in one launch
+// (gemm_i8_pipe2_mixed).  A tile's cost, in units of one 256x256x64 k-tile of
+// MFMA work: its K/64 k-tiles plus about 6 units of prologue and epilogue,
+// scaled by the tile's relative cost per k-tile (1 for 256x256; 0.55 for
+// 256x128; 0.35 for 128x128, whose LDS reads per MFMA are twice those of
+// 256x256).  A plan's cost is the finishing time of its tiles dealt in
+// launch order to the CU that frees first (the dispatcher's order).
 struct TileChoice {
   int bm, bn;
   double unit;
@@ -266,20 +292,77 @@ constexpr TileChoice kTiles[] = {{256, 256, 1.0}, {256, 128, 0.55}, {128, 128, 0
 
 struct PipePlan {
   int bm = 0, bn = 0;
+  int nw = 0;  // > 0: mixed launch, 256-wide tiles over the first 256 nw columns, 256x128 after
 };
+
+// Finishing time of `n1` tasks of length d1 then `n2` of length d2, each
+// dealt to the earliest-free of `cus` identical CUs.  CUs that free at the
+// same time are kept as one group, so the loop runs once per group and round.
+double list_makespan(long n1, double d1, long n2, double d2, int cus) {
+  struct Grp {
+    double t;
+    long n;
+  };
+  Grp g[8];
+  int ng = 1;
+  g[0] = {0.0, cus};
+  auto deal = [&](long tasks, double d) {
+    while (tasks > 0) {
+      int k = 0;  // earliest group
+      for (int i = 1; i < ng; ++i)
+        if (g[i].t < g[k].t) k = i;
+      const long take = tasks < g[k].n ? tasks : g[k].n;
+      tasks -= take;
+      const double t_end = g[k].t + d;
+      if (take == g[k].n) {
+        g[k].t = t_end;
+      } else {
+        g[k].n -= take;
+        int j = -1;  // merge with a group ending at the same time, else a new one
+        for (int i = 0; i < ng; ++i)
+          if (g[i].t == t_end) j = i;
+        if (j >= 0)
+          g[j].n += take;
+        else if (ng < 8)
+          g[ng++] = {t_end, take};
+        else
+          return false;
+      }
+    }
+    return true;
+  };
+  if (!deal(n1, d1) || !deal(n2, d2)) return 1e300;  // (more than 8 distinct finishing times: not planned)
+  double t = 0;
+  for (int i = 0; i < ng; ++i) t = g[i].t > t ? g[i].t : t;
+  return t;
+}
 
 PipePlan plan_pipe(int M, int N, int K, int cus) {
   PipePlan best;
   if (K % BK != 0 || cus < 1) return best;
-  double best_cost = 0;
+  const double work = K / BK + 6.0;
+  // lowest finishing time; among equal ones, the least total CU time (fewer
+  // of the costlier narrow tiles, less energy under the power limit)
+  double best_cost = 0, best_total = 0;
+  auto consider = [&](double cost, double total, PipePlan p) {
+    if (best.bm == 0 || cost < best_cost - 1e-9 || (cost < best_cost + 1e-9 && total < best_total - 1e-9)) {
+      best_cost = cost;
+      best_total = total;
+      best = p;
+    }
+  };
   for (const TileChoice& t : kTiles) {
     if (M % t.bm != 0 || N % t.bn != 0) continue;
     const long tiles = (long)(M / t.bm) * (N / t.bn);
-    const double cost = (double)((tiles + cus - 1) / cus) * t.unit * (K / BK + 6.0);
-    if (best.bm == 0 || cost < best_cost - 1e-9) {
-      best_cost = cost;
-      best.bm = t.bm;
-      best.bn = t.bn;
+    consider((double)((tiles + cus - 1) / cus) * t.unit * work, tiles * t.unit * work, PipePlan{t.bm, t.bn, 0});
+  }
+  // mixed 256x256 + 256x128 (the pair-staged kernel: K % 128 == 0)
+  if (M % 256 == 0 && N % 128 == 0 && N > 256 && K % 128 == 0) {
+    const long tm = M / 256;
+    for (int nw = 1; 256 * nw < N; ++nw) {
+      const long wide = tm * nw, narrow = tm * ((N - 256 * nw) / 128);
+      const double dw = kTiles[0].unit * work, dn = kTiles[1].unit * work;
+      consider(list_makespan(wide, dw, narrow, dn, cus), wide * dw + narrow * dn, PipePlan{256, 256, nw});
     }
   }
   return best;
@@ -303,7 +386,12 @@ int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_p
   const PipePlan p = dense_ok ? plan_pipe(M, N, K, ctx->cus) : PipePlan{};
   *plan = miaie_gemm_plan{};
   plan->threads = 256;
-  if (p.bm) {
+  if (p.bm && p.nw) {
+    plan->kernel = MIAIE_KERNEL_PIPE_MIXED;
+    plan->tile_m = 256;
+    plan->tile_n = 256;
+    plan->workgroups = (M / 256) * (p.nw + (N - 256 * p.nw) / 128);
+  } else if (p.bm) {
     plan->kernel = MIAIE_KERNEL_PIPE;
     plan->tile_m = p.bm;
     plan->tile_n = p.bn;
@@ -321,7 +409,14 @@ int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_p
 int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
                    int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu) {
   miaie_gemm_plan plan;
-  plan_gemm_i8(ctx, M, N, K, pipe_operands_ok(A, B, Y, C, K, lda, ldb, ldy, ldc), &plan);
+  const bool dense_ok = pipe_operands_ok(A, B, Y, C, K, lda, ldb, ldy, ldc);
+  plan_gemm_i8(ctx, M, N, K, dense_ok, &plan);
+  if (plan.kernel == MIAIE_KERNEL_PIPE_MIXED) {
+    const int nw = plan_pipe(M, N, K, ctx->cus).nw;
+    b_nt ? launch_pipe_mixed<true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw)
+         : launch_pipe_mixed<false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw);
+    return check_launch(ctx, "gemm_i8_pipe2_mixed");
+  }
   if (plan.kernel == MIAIE_KERNEL_PIPE) {
     hipStream_t st = ctx->stream;
     const int bm = plan.tile_m, bn = plan.tile_n;

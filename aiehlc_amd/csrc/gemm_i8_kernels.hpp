@@ -513,19 +513,18 @@ struct Pipe2Geom {
 // end, then the 100 MHz wall clock at the start and the end.
 constexpr int PROBE_WORDS = 6;
 
-template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED = false>
-__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
-    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
-    int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
-    int relu, unsigned long long* __restrict__ probe) {
-  unsigned long long t0 = 0, r0 = 0, t1 = 0, t2 = 0;
-  if constexpr (TIMED) {
-    t0 = __builtin_amdgcn_s_memtime();
-    r0 = __builtin_amdgcn_s_memrealtime();
-  }
+// One BM x BN output tile (tm, tn) of the pair-staged pipeline, in the
+// workgroup's LDS `lds` (at least Pipe2Geom<BM, BN, NW>::LDS_BYTES, 1 KiB
+// aligned).  t0 / r0: the clocks at the workgroup's start (TIMED only).
+template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED>
+__device__ __forceinline__ void pipe2_tile(int8_t* lds, int tm, int tn, const int8_t* __restrict__ A,
+                                           const int8_t* __restrict__ B, int8_t* __restrict__ Y,
+                                           int32_t* __restrict__ C, int K, int lda, int ldb, int ldy, int ldc,
+                                           int shift, int relu, unsigned long long* __restrict__ probe,
+                                           unsigned long long t0, unsigned long long r0) {
+  unsigned long long t1 = 0, t2 = 0;
   using G = Pipe2Geom<BM, BN, NW>;
   constexpr bool WRITE_Y = YQ != Y_NONE;
-  __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS_BYTES];
   const uint32_t lds0 = dev::lds_addr(lds);
   int8_t* const bl = lds + G::A_REGION;  // B stages
 
@@ -533,8 +532,6 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  int tm, tn;
-  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT = K / BK;  // even
 
@@ -772,6 +769,53 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
 #pragma unroll
     for (int i = 0; i < PROBE_WORDS; ++i) v = lane == i ? rec[i] : v;
     if (lane < PROBE_WORDS) probe[((size_t)blockIdx.x * NW + wave) * PROBE_WORDS + lane] = v;
+  }
+}
+
+template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED = false>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
+    int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
+    int relu, unsigned long long* __restrict__ probe) {
+  unsigned long long t0 = 0, r0 = 0;
+  if constexpr (TIMED) {
+    t0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  __shared__ __attribute__((aligned(1024))) int8_t lds[Pipe2Geom<BM, BN, NW>::LDS_BYTES];
+  int tm, tn;
+  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
+  pipe2_tile<BM, BN, NW, B_NT, YQ, WRITE_C, TIMED>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift, relu,
+                                                    probe, t0, r0);
+}
+
+// Mixed tile widths in one launch: the first M/256 * nw workgroups take the
+// 256 x 256 tiles of output columns [0, 256 nw), the rest the 256 x 128
+// tiles of columns [256 nw, N).  Workgroups are dispatched in order, so the
+// narrow tiles fill the CUs the wide ones leave idle and then the CUs they
+// free.  For shapes whose 256-wide tiles would leave most of a round empty
+// (the MLP's 2048 x 11008 up-projection: 344 wide tiles on 256 CUs, or 688
+// narrow ones, 2.7 rounds) the planner picks the split (plan_pipe).
+template <bool B_NT, int YQ, bool WRITE_C>
+__global__ __launch_bounds__(256, 1) void gemm_i8_pipe2_mixed(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
+    int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
+    int relu, int nw) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[Pipe2Geom<256, 256, 4>::LDS_BYTES];
+  static_assert(Pipe2Geom<256, 128, 4>::LDS_BYTES <= Pipe2Geom<256, 256, 4>::LDS_BYTES, "narrow tile fits");
+  const int TM = M / 256, nwide = TM * nw;
+  const int b = blockIdx.x;
+  int tm, tn;
+  if (b < nwide) {
+    dev::tile_coords<4>(b, TM, nw, tm, tn);
+    pipe2_tile<256, 256, 4, B_NT, YQ, WRITE_C, false>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift, relu,
+                                                       nullptr, 0, 0);
+  } else {
+    dev::tile_coords<4>(b - nwide, TM, (N - 256 * nw) / 128, tm, tn);
+    const size_t c0 = (size_t)256 * nw;  // first column of the narrow tiles
+    pipe2_tile<256, 128, 4, B_NT, YQ, WRITE_C, false>(lds, tm, tn, A, B_NT ? B + c0 * ldb : B + c0,
+                                                       Y ? Y + c0 : nullptr, C ? C + c0 : nullptr, K, lda, ldb,
+                                                       ldy, ldc, shift, relu, nullptr, 0, 0);
   }
 }
 

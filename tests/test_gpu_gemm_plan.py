@@ -21,9 +21,13 @@ def test_planner_choices(ctx):
     # one GPU's 512-row share of the 4096^3 GEMM: more, smaller tiles
     shard = ctx.plan_gemm_i8(512, 4096, 4096)
     assert (shard["tile_m"], shard["tile_n"], shard["workgroups"]) == (128, 128, 128)
-    # the MLP's projections keep 256-row tiles
-    assert (ctx.plan_gemm_i8(2048, 11008, 4096)["tile_m"], ctx.plan_gemm_i8(2048, 11008, 4096)["tile_n"]) == (256, 128)
-    assert ctx.plan_gemm_i8(2048, 4096, 11008)["tile_m"] == 256
+    # the MLP's up-projection: 256 wide tiles fill one round, 176 narrow ones
+    # the next (344 wide tiles would take 2 rounds, 688 narrow ones 2.7)
+    up = ctx.plan_gemm_i8(2048, 11008, 4096)
+    assert (up["kernel"], up["tile_m"], up["tile_n"], up["workgroups"]) == (mi.KERNEL_PIPE_MIXED, 256, 256, 256 + 176)
+    # its down-projection: exactly one round of 256x128 tiles
+    down = ctx.plan_gemm_i8(2048, 4096, 11008)
+    assert (down["kernel"], down["tile_m"], down["tile_n"]) == (mi.KERNEL_PIPE, 256, 128)
     # shapes the pipelined kernel cannot take
     assert ctx.plan_gemm_i8(100, 50, 30)["kernel"] == mi.KERNEL_TILE64
     assert ctx.plan_gemm_i8(128, 128, 100)["kernel"] == mi.KERNEL_TILE64
@@ -32,7 +36,8 @@ def test_planner_choices(ctx):
     prev = ctx.plan_set_cus(1)
     try:
         assert (ctx.plan_gemm_i8(512, 512, 256)["tile_m"], ctx.plan_gemm_i8(512, 512, 256)["tile_n"]) == (256, 256)
-        assert ctx.plan_gemm_i8(256, 384, 256)["tile_n"] == 128
+        assert ctx.plan_gemm_i8(256, 384, 256)["kernel"] == mi.KERNEL_PIPE_MIXED  # one wide + one narrow tile
+        assert ctx.plan_gemm_i8(256, 384, 192)["tile_n"] == 128  # K % 128 != 0: no mixed kernel
         assert ctx.plan_gemm_i8(128, 256, 256)["tile_m"] == 128
     finally:
         assert ctx.plan_set_cus(prev) == 1
@@ -81,10 +86,11 @@ def test_128_tiles_match_the_oracle(ctx, M, N, K, layout):
 # over the last six k-tiles and in the prologue below 6 k-tiles), other
 # multiples of 64 the per-k-tile kernel.  Every k-tile count from the
 # smallest up to well past the steady state, at each tile width (planned for
-# one CU, M x N picks 256x256, 256x128 and 128x128), both B layouts and every
-# output mode.
+# one CU, M x N picks 256x256, 256x128 and 128x128, and 256 x 384 one wide
+# and one narrow tile in a mixed launch), both B layouts and every output
+# mode.
 K_SWEEP = [64, 128, 192, 256, 320, 384, 512, 640, 768, 896, 1024, 1152, 1280, 2176, 2240]
-TILE_SHAPES = [(512, 512), (256, 384), (128, 256)]
+TILE_SHAPES = [(512, 512), (256, 128), (128, 256), (256, 384)]
 
 
 @pytest.mark.parametrize("K", K_SWEEP)
@@ -103,9 +109,13 @@ def test_pipelined_k_sweep(ctx, K, MN, layout):
 def _k_sweep(ctx, M, N, K, MN, layout):
     plan = ctx.plan_gemm_i8(M, N, K)
     print(f"[case] k-sweep gemm {M}x{N}x{K} layout {layout} plan {plan}", flush=True)
-    assert plan["kernel"] == mi.KERNEL_PIPE
-    assert (plan["tile_m"], plan["tile_n"]) == {(512, 512): (256, 256), (256, 384): (256, 128),
-                                                (128, 256): (128, 128)}[MN]
+    if MN == (256, 384) and K % 128 == 0:
+        # one 256x256 and one 256x128 tile in one launch (the pair-staged kernel needs K % 128 == 0)
+        assert (plan["kernel"], plan["workgroups"]) == (mi.KERNEL_PIPE_MIXED, 2)
+    else:
+        assert plan["kernel"] == mi.KERNEL_PIPE
+        assert (plan["tile_m"], plan["tile_n"]) == {(512, 512): (256, 256), (256, 128): (256, 128),
+                                                    (128, 256): (128, 128), (256, 384): (256, 128)}[MN]
     rng = np.random.default_rng(7 * K + M + layout)
     A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
     B = rng.integers(-128, 128, size=(N, K) if layout == mi.B_NT else (K, N), dtype=np.int8)
@@ -213,3 +223,40 @@ def test_ragged_fallback_matches_the_oracle(ctx, M, N, K, layout, lda_pad):
             b.free()
     for b in (dA, dB, dC):
         b.free()
+
+
+# Mixed launches (gemm_i8_pipe2_mixed): 256x256 tiles over the first
+# columns, 256x128 tiles over the rest.  Planned for fewer CUs where that
+# makes small shapes choose the mix; every output mode and both B layouts,
+# bit-exact against the oracle.
+MIXED = [(512, 1408, 256, 16, mi.B_NN), (512, 1408, 256, 16, mi.B_NT), (256, 640, 384, 2, mi.B_NN),
+         (768, 896, 128, 5, mi.B_NT), (2048, 11008, 256, 256, mi.B_NN)]
+
+
+@pytest.mark.parametrize("M,N,K,cus,layout", MIXED)
+def test_mixed_tiles_match_the_oracle(ctx, M, N, K, cus, layout):
+    prev = ctx.plan_set_cus(cus)
+    try:
+        plan = ctx.plan_gemm_i8(M, N, K)
+        print(f"[case] mixed gemm {M}x{N}x{K} cus {cus} layout {layout} plan {plan}", flush=True)
+        assert plan["kernel"] == mi.KERNEL_PIPE_MIXED, plan
+        rng = np.random.default_rng(M * 3 + N + K + layout)
+        A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+        B = rng.integers(-128, 128, size=(N, K) if layout == mi.B_NT else (K, N), dtype=np.int8)
+        dA, dB = ctx.upload(A), ctx.upload(B)
+        dC, dY, dY2, dC2 = (ctx.empty((M, N), np.int32), ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int8),
+                            ctx.empty((M, N), np.int32))
+        ctx.gemm_i8_i32(dA, dB, dC, M, N, K, b_layout=layout)          # C only
+        ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, layout)    # Y only (int16-saturation form)
+        ctx.gemm_i8_rq(dA, dB, dY2, M, N, K, 5, True, dC2, layout)      # Y + C, med3 form, ReLU
+        ctx.wait(60_000)
+        C, Y, Y2, C2 = ctx.download(dC), ctx.download(dY), ctx.download(dY2), ctx.download(dC2)
+        for b in (dA, dB, dC, dY, dY2, dC2):
+            b.free()
+    finally:
+        ctx.plan_set_cus(prev)
+    Co = oracle.gemm_i8(A, B, b_nt=layout == mi.B_NT)
+    assert np.array_equal(C, Co)
+    assert np.array_equal(C2, Co)
+    assert np.array_equal(Y, oracle.requant(Co, 10))
+    assert np.array_equal(Y2, oracle.requant(Co, 5, relu=True))
