@@ -321,7 +321,10 @@ extern "C" int miaie_plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, miaie_gem
   if (rc) return rc;
   MIAIE_CHECK_NOT_NULL(ctx, plan);
   if (M < 1 || N < 1 || K < 1) return fail(ctx, MIAIE_EINVAL, "miaie_plan_gemm_i8: M=%d N=%d K=%d", M, N, K);
-  return plan_gemm_i8(ctx, M, N, K, (K % 16 == 0) && (N % 16 == 0) && K < (1 << 16), plan);
+  // the operand conditions of miaie_gemm_i8_rq on dense NN operands (lda = K,
+  // ldb = ldy = N): 16-byte rows, strides below 2^25, and K < 2^16 for the
+  // requantizing epilogue's shortcut
+  return plan_gemm_i8(ctx, M, N, K, (K % 16 == 0) && (N % 16 == 0) && K < (1 << 16) && N < (1 << 25), plan);
 }
 
 extern "C" int miaie_plan_set_cus(miaie_ctx* ctx, int cus, int* previous) {

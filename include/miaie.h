@@ -99,10 +99,12 @@ MIAIE_API int miaie_wait(miaie_ctx* ctx, int timeout_ms);
 #define MIAIE_KERNEL_PIPE_MIXED 2 /* pipelined kernel, 256x256 tiles over the first columns and 256x128
                                      tiles over the rest, in one launch (tile_m = tile_n = 256) */
 
-/* How miaie_gemm_i8_* would run an M x N x K product on this context with
- * dense 16-byte-aligned operands (the tiling planner: the grid
+/* How miaie_gemm_i8_rq would run an M x N x K product on this context with
+ * dense 16-byte-aligned NN operands (the tiling planner: the grid
  * decomposition and tile choice that stand in for the reference's tiling
- * prototype, src/mlir/mlirfront/tilinglinalg/tilinglinalg.cpp:38-146). */
+ * prototype, src/mlir/mlirfront/tilinglinalg/tilinglinalg.cpp:38-146).
+ * miaie_gemm_i8_i32 runs the same plan, except that for K >= 2^16, where the
+ * requantizing entry takes the 64x64 kernel, it keeps the pipelined one. */
 typedef struct {
   int kernel;         /* MIAIE_KERNEL_* */
   int tile_m, tile_n; /* workgroup output tile */
