@@ -13,8 +13,12 @@
 //                   by global_load_lds_dwordx4; the row-major (NN) B operand
 //                   is transposed by ds_read_b64_tr_b8 on its way out of LDS.
 //                   XCD-aware tile order.  M % BM == N % BN == K % 64 == 0.
-//   gemm_i8_pipe2   the same with A staged two k-tiles at a time, so A copies
-//                   move whole cache lines (256-row tiles, K % 128 == 0).
+//   gemm_i8_pipe16  256-row tiles with K % 128 == 0: the same pipeline with A
+//                   staged two k-tiles at a time (A copies move whole cache
+//                   lines), multiplied on v_mfma_i32_16x16x64_i8, which runs
+//                   at a higher clock than the 32x32 form under the power
+//                   limit; gemm_i8_pipe16_mixed puts 256x256 and 256x128
+//                   tiles in one launch.
 //   gemm_i8_tile64p 64x64x64 tile for K % 16 == 0 and 16-byte aligned rows:
 //                   clamped vector loads, next k-tile prefetched into
 //                   registers.
@@ -212,24 +216,22 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
     hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu,
                        (unsigned long long*)nullptr);
   };
-  // 256-row tiles with K a multiple of 128: A staged two k-tiles at a time
-  // (gemm_i8_pipe2; 256x256 4096^3 68.9 -> 66.4 us, the MLP's 256x128
-  // projections 6-10% faster).  At 128x128, where half the CUs run at a higher
-  // clock, it measured 4% slower, so that tile keeps gemm_i8_pipe.
+  // 256-row tiles with K a multiple of 128: A staged two k-tiles at a time,
+  // 16x16x64 MFMAs (gemm_i8_pipe16).  128x128 tiles keep gemm_i8_pipe.
   if constexpr (BM == 256) {
     if (K % 128 == 0) {
       if (C) {
         switch (yq) {
-          case Y_NONE: go2(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_NONE, true>); break;
-          case Y_MED3: go2(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_MED3, true>); break;
-          case Y_HI: go2(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_HI, true>); break;
-          default: go2(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_HI_RELU, true>); break;
+          case Y_NONE: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_NONE, true>); break;
+          case Y_MED3: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_MED3, true>); break;
+          case Y_HI: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI, true>); break;
+          default: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI_RELU, true>); break;
         }
       } else {
         switch (yq) {
-          case Y_MED3: go2(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_MED3, false>); break;
-          case Y_HI: go2(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_HI, false>); break;
-          default: go2(gemm_i8_pipe2<BM, BN, NW, B_NT, Y_HI_RELU, false>); break;
+          case Y_MED3: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_MED3, false>); break;
+          case Y_HI: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI, false>); break;
+          default: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI_RELU, false>); break;
         }
       }
       return;
@@ -261,16 +263,16 @@ void launch_pipe_mixed(hipStream_t st, const int8_t* A, const int8_t* B, int8_t*
   };
   if (C) {
     switch (yq) {
-      case Y_NONE: go(gemm_i8_pipe2_mixed<B_NT, Y_NONE, true>); break;
-      case Y_MED3: go(gemm_i8_pipe2_mixed<B_NT, Y_MED3, true>); break;
-      case Y_HI: go(gemm_i8_pipe2_mixed<B_NT, Y_HI, true>); break;
-      default: go(gemm_i8_pipe2_mixed<B_NT, Y_HI_RELU, true>); break;
+      case Y_NONE: go(gemm_i8_pipe16_mixed<B_NT, Y_NONE, true>); break;
+      case Y_MED3: go(gemm_i8_pipe16_mixed<B_NT, Y_MED3, true>); break;
+      case Y_HI: go(gemm_i8_pipe16_mixed<B_NT, Y_HI, true>); break;
+      default: go(gemm_i8_pipe16_mixed<B_NT, Y_HI_RELU, true>); break;
     }
   } else {
     switch (yq) {
-      case Y_MED3: go(gemm_i8_pipe2_mixed<B_NT, Y_MED3, false>); break;
-      case Y_HI: go(gemm_i8_pipe2_mixed<B_NT, Y_HI, false>); break;
-      default: go(gemm_i8_pipe2_mixed<B_NT, Y_HI_RELU, false>); break;
+      case Y_MED3: go(gemm_i8_pipe16_mixed<B_NT, Y_MED3, false>); break;
+      case Y_HI: go(gemm_i8_pipe16_mixed<B_NT, Y_HI, false>); break;
+      default: go(gemm_i8_pipe16_mixed<B_NT, Y_HI_RELU, false>); break;
     }
   }
 }
@@ -278,7 +280,7 @@ void launch_pipe_mixed(hipStream_t st, const int8_t* A, const int8_t* B, int8_t*
 // Tiling planner for the pipelined kernel: picks the workgroup tile
 // (BM x BN) among 256x256, 256x128 and 128x128 for an M x N x K product on
 // `cus` compute units, or a mix of 256x256 and 256x128 tiles in one launch
-// (gemm_i8_pipe2_mixed).  A tile's cost, in units of one 256x256x64 k-tile of
+// (gemm_i8_pipe16_mixed).  A tile's cost, in units of one 256x256x64 k-tile of
 // MFMA work: its K/64 k-tiles plus about 6 units of prologue and epilogue,
 // scaled by the tile's relative cost per k-tile (1 for 256x256; 0.55 for
 // 256x128; 0.35 for 128x128, whose LDS reads per MFMA are twice those of
@@ -415,7 +417,7 @@ int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, 
     const int nw = plan_pipe(M, N, K, ctx->cus).nw;
     b_nt ? launch_pipe_mixed<true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw)
          : launch_pipe_mixed<false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw);
-    return check_launch(ctx, "gemm_i8_pipe2_mixed");
+    return check_launch(ctx, "gemm_i8_pipe16_mixed");
   }
   if (plan.kernel == MIAIE_KERNEL_PIPE) {
     hipStream_t st = ctx->stream;

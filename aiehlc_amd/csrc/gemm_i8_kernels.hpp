@@ -1,8 +1,8 @@
 // int8 GEMM device code shared by the library (gemm_i8.hip) and the
 // in-kernel clock probe (probes/gemm_span.hip): the requantize epilogues and
-// the pipelined kernels gemm_i8_pipe and gemm_i8_pipe2.  The kernel list,
-// tiling and operand-role conventions are described at the top of
-// gemm_i8.hip.
+// the pipelined kernels gemm_i8_pipe, gemm_i8_pipe16 and
+// gemm_i8_pipe16_mixed.  The kernel list, tiling and operand-role conventions
+// are described at the top of gemm_i8.hip.
 #pragma once
 
 #include <type_traits>
@@ -465,8 +465,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
                                         rnd - acc0);
 }
 
-// ------------------------------------------------------ pair-staged tile
-// gemm_i8_pipe with A staged two k-tiles at a time.  A row-major A tile
+// ------------------------------------------------------ pair-staged tiles
+// The pipeline of gemm_i8_pipe with A staged two k-tiles at a time.  A row-major A tile
 // row contributes 64 bytes per k-tile, so a per-k-tile copy touches every
 // 128-byte line at half use; the L1 fetches whole lines, the address path
 // handles 16 lines per 1 KiB copy, and the A stream costs twice its bytes on
@@ -488,12 +488,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
 // last tiles (dev::pair_vm).
 constexpr int NA2 = 3;
 
+// Stages and copy geometry of the pair-staged pipeline (NW waves).
 template <int BM, int BN, int NW>
-struct Pipe2Geom {
-  static constexpr int THREADS = 64 * NW;
-  static constexpr int WAVES_N = NW / 2;
-  static constexpr int WM = BM / 2, WN = BN / WAVES_N;
-  static constexpr int NI = WM / 32, NJ = WN / 32, NMF = NI * NJ;
+struct PairGeom {
   static constexpr int A2_BYTES = BM * 128;                 // one A pair stage
   static constexpr int A_REGION = NA2 * A2_BYTES;
   static constexpr int B_BYTES = BN * BK;                   // one B stage
@@ -503,8 +500,7 @@ struct Pipe2Geom {
   static constexpr int QA = A_CP2 / 4;                      // ... per quarter (per phase)
   static constexpr int B_CP = B_BYTES / CP_BYTES;           // B copies per thread per k-tile
   static constexpr int B_CP0 = (B_CP + 1) / 2, B_CP1 = B_CP - B_CP0;
-  static constexpr int CP = A_CP2 / 2 + B_CP;               // copies per thread per k-tile
-  static_assert(NI >= 1 && NJ >= 1 && B_CP >= 1 && A_CP2 % 4 == 0 && QA >= 1, "pair-staged geometry");
+  static_assert(B_CP >= 1 && A_CP2 % 4 == 0 && QA >= 1, "pair-staged geometry");
   static_assert(LDS_BYTES <= 163840 && BM * BN <= LDS_BYTES, "pair-staged LDS budget");
 };
 
@@ -513,20 +509,96 @@ struct Pipe2Geom {
 // end, then the 100 MHz wall clock at the start and the end.
 constexpr int PROBE_WORDS = 6;
 
-// One BM x BN output tile (tm, tn) of the pair-staged pipeline, in the
-// workgroup's LDS `lds` (at least Pipe2Geom<BM, BN, NW>::LDS_BYTES, 1 KiB
-// aligned).  t0 / r0: the clocks at the workgroup's start (TIMED only).
+// ---------------------------------------- pair-staged tile on 16x16x64 MFMA
+// One BM x BN output tile (256 x 256 or 256 x 128; 4 waves of BM/2 x BN/2)
+// of the pair-staged pipeline above, multiplied on v_mfma_i32_16x16x64_i8.
+// v_mfma_i32_32x32x32_i8 does the same MACs per cycle, but the 16x16 form
+// reads and writes half as many accumulator bits per MAC, and these boxes run
+// power-limited: register-only streams of random int8 operands sustained
+// 3.8 POP/s at a 1.9 GHz shader clock on the 16x16 form against 3.3 POP/s at
+// 1.65 GHz on the 32x32 form, same GPU, same run (probes/mfma_ceiling).
+//
+// Copies (global_load_lds_dwordx4, 1 KiB per wave): A copy x of wave w fills
+// the 1 KiB block NW*x + w of a pair stage, rows 8(NW*x + w) + lane/8,
+// physical chunk lane%8 of the row's 128 bytes, holding logical chunk
+// (lane%8) ^ ((row >> 1) & 7); B copies as in gemm_i8_pipe, with the NN
+// swizzle bswz16 below.
+//
+// A wave's WM x WN quarter is NI x NJ blocks of 16 x 16 (NI = WM/16, NJ =
+// WN/16), and one 64-wide k-tile is one k-step.  Block (i, j) of k-tile t is
+// multiplied in phase 1 of tile t for i < NI/2 and in phase 2 for i >= NI/2,
+// column-block-major (j outer, i inner) in both phases:
+//   phase 1: A fragments 0 .. NI/2-1 (alo) and the B fragments, while A
+//            fragments NI/2 .. NI-1 of tile t (ahi) are read;
+//   barrier (tile t+1 landed);
+//   phase 2: ahi and the B fragments, while alo and the B fragments of tile
+//            t+1 are read, B fragment j right after the last MFMA that uses
+//            tile t's B fragment j, into the same registers.
+// One set of A and B fragment registers then suffices (64 VGPRs), which
+// keeps the 256 accumulators in the AGPRs.  Tile t's fragments are read
+// between phase 2 of tile t-1 and phase 1 of tile t, and the copy schedule
+// above overwrites a stage only after the barrier that follows its last read.
+//
+// Fragments: lane l holds, for A fragment i, row 16i + l%16 of the wave's
+// rows, k = 16(l/16) .. +16 (logical 16-byte chunk l/16 of the k-tile); for B
+// fragment j, column 16j + l%16, the same k.  The accumulator of block (i, j)
+// (srcA = B fragment, srcB = A fragment) holds in lane l row 16i + l%16,
+// columns 16j + 4(l/16) + 0..3.  NN B fragments are two ds_read_b64_tr_b8
+// halves (k 16(l/16) + 0..7 and + 8..15); a 32-lane read then spans k-rows
+// r and r + 16, so the B stage swizzle also XORs k-row bit 4 into the chunk
+// index (bswz16), which keeps those reads conflict-free.
+template <int BN>
+__device__ __forceinline__ int bswz16(int k) {
+  return bswz<BN>(k) | ((k >> 4) & 1);
+}
+
+// acc += srcA x srcB in place.  The compiler's own form of this instruction
+// writes a result register set distinct from the accumulator's, and with all
+// 256 AGPRs holding a 128x128 wave tile it then shuttles accumulators through
+// VGPRs (hundreds of extra moves per k-tile, and spills); written out, the
+// accumulator is updated in place.  Operands come straight from LDS reads
+// (the compiler's lgkmcnt waits see the asm's register uses); the end of the
+// main loop waits out the last MFMAs' latency before any accumulator is read
+// (mfma16_drain).
+__device__ __forceinline__ void mfma16(v4i& acc, v4i a, v4i b) {
+  asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// 8-pass MFMA results are readable by VALU after 11 wait states (gfx950);
+// 24 here, with nothing scheduled across.
+__device__ __forceinline__ void mfma16_drain() {
+  dev::sched_fence();
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  dev::sched_fence();
+}
+
+template <int BM, int BN, int NW>
+struct Pipe16Geom {
+  using G2 = PairGeom<BM, BN, NW>;  // stages and copy geometry
+  static constexpr int WAVES_N = NW / 2;
+  static constexpr int WM = BM / 2, WN = BN / WAVES_N;
+  static constexpr int NI = WM / 16, NJ = WN / 16, HI = NI / 2;
+  static constexpr int PH = HI * NJ;  // MFMAs per phase
+  static_assert(NI % 2 == 0 && NJ >= 1 && HI * 16 * 2 == WM, "16x16 blocks per wave");
+};
+
 template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED>
-__device__ __forceinline__ void pipe2_tile(int8_t* lds, int tm, int tn, const int8_t* __restrict__ A,
-                                           const int8_t* __restrict__ B, int8_t* __restrict__ Y,
-                                           int32_t* __restrict__ C, int K, int lda, int ldb, int ldy, int ldc,
-                                           int shift, int relu, unsigned long long* __restrict__ probe,
-                                           unsigned long long t0, unsigned long long r0) {
+__device__ __forceinline__ void pipe16_tile(int8_t* lds, int tm, int tn, const int8_t* __restrict__ A,
+                                            const int8_t* __restrict__ B, int8_t* __restrict__ Y,
+                                            int32_t* __restrict__ C, int K, int lda, int ldb, int ldy, int ldc,
+                                            int shift, int relu, unsigned long long* __restrict__ probe,
+                                            unsigned long long t0, unsigned long long r0) {
   unsigned long long t1 = 0, t2 = 0;
-  using G = Pipe2Geom<BM, BN, NW>;
+  using G = typename Pipe16Geom<BM, BN, NW>::G2;
+  using H = Pipe16Geom<BM, BN, NW>;
+  constexpr int NI = H::NI, NJ = H::NJ, HI = H::HI, PH = H::PH;
   constexpr bool WRITE_Y = YQ != Y_NONE;
+  // LDS: the four B stages first, then the three A pair stages.  A B
+  // fragment read is then its lane's base address plus a compile-time offset
+  // below 2^16 (the ds_read offset field) wherever the stage is known.
+  constexpr int B_REGION = STAGES * G::B_BYTES;
+  constexpr int B_MASK = B_REGION - 1;
+  static_assert(B_REGION + G::A_REGION == G::LDS_BYTES && (B_REGION & B_MASK) == 0, "B stages first");
   const uint32_t lds0 = dev::lds_addr(lds);
-  int8_t* const bl = lds + G::A_REGION;  // B stages
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -535,135 +607,122 @@ __device__ __forceinline__ void pipe2_tile(int8_t* lds, int tm, int tn, const in
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT = K / BK;  // even
 
-  // ---- copy assignment.  A copy x of wave w fills the 1 KiB block NW*x + w
-  // of a pair stage: rows 8*(NW*x + w) + lane/8, physical chunk lane%8 of the
-  // row's 128 bytes, holding logical chunk (lane%8) ^ aswz(row) with
-  // aswz(row) = (row >> 1) & 7 (= 4*(w&1) + lane/16 for every x).  The MFMA
-  // fragment read (16 consecutive rows at one logical chunk) then touches 16
-  // distinct 16-byte bank groups.  B copies as in gemm_i8_pipe.
+  // ---- copies.  A copy is one global_load_lds_dwordx4 from a wave-uniform
+  // source pointer (per operand and k-tile) plus a per-lane offset; NN B
+  // copies whose k-rows differ in bit 4 differ in bswz16.
   const int a_r = 8 * wave + (lane >> 3);
   const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 7) ^ ((a_r >> 1) & 7));
-  const int8_t* const a_base = A + (size_t)m0 * lda;
-  uint32_t b_voff;
-  const int8_t* b_base;
   constexpr int B_ROWS_PER_CP = B_NT ? 16 * NW : 1024 * NW / BN;
+  uint32_t b_voff[2];
   if constexpr (B_NT) {
     const int b_r = 16 * wave + (lane >> 2);
-    b_voff = (uint32_t)b_r * ldb + 16 * ((lane & 3) ^ swz(b_r));
-    b_base = B + (size_t)n0 * ldb;
+    b_voff[0] = b_voff[1] = (uint32_t)b_r * ldb + 16 * ((lane & 3) ^ swz(b_r));
   } else {
+    static_assert(B_ROWS_PER_CP == 16 || B_ROWS_PER_CP % 32 == 0, "k-row bit 4 per NN B copy");
     constexpr int CPR = BN / 16;
     const int b_r = (1024 / BN) * wave + lane / CPR;
-    b_voff = (uint32_t)b_r * ldb + 16 * ((lane % CPR) ^ bswz<BN>(b_r));
-    b_base = B + n0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      b_voff[e] = (uint32_t)b_r * ldb + 16 * ((lane % CPR) ^ bswz16<BN>(b_r + (B_ROWS_PER_CP == 16 ? 16 * e : 0)));
   }
-  // copy x (< A_CP2) of A pair p; copy x (< B_CP) of B k-tile kt
-  auto copy_a = [&](int p, int x) {
-    const uint32_t st = lds0 + (p % NA2) * G::A2_BYTES + 1024 * wave + G::CP_BYTES * x;
-    dev::gload_lds16(a_base + (size_t)p * 128 + (size_t)(8 * NW * x) * lda, a_voff, st);
+  const int8_t* const a_base = A + (size_t)m0 * lda;
+  const int8_t* const b_base = B_NT ? B + (size_t)n0 * ldb : B + n0;
+  const size_t b_kstep = B_NT ? (size_t)BK : (size_t)BK * ldb;  // B source per k-tile
+  const uint32_t ldsw = lds0 + 1024 * wave;
+  // copy x of an A pair (source src) into the pair stage at byte st of the A region
+  auto copy_a = [&](const int8_t* src, uint32_t st, int x) __attribute__((always_inline)) {
+    dev::gload_lds16(src + (size_t)(8 * NW * x) * lda, a_voff, ldsw + B_REGION + st + G::CP_BYTES * x);
   };
-  auto copy_b = [&](int kt, int x) {
-    const uint32_t st = lds0 + G::A_REGION + (kt & (STAGES - 1)) * G::B_BYTES + 1024 * wave + G::CP_BYTES * x;
-    const int8_t* bb = B_NT ? b_base + (size_t)kt * BK : b_base + (size_t)kt * BK * ldb;
-    dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * x) * ldb, b_voff, st);
+  // copy x of a B k-tile (source src) into the B stage at byte st
+  auto copy_b = [&](const int8_t* src, uint32_t st, int x) __attribute__((always_inline)) {
+    dev::gload_lds16(src + (size_t)(B_ROWS_PER_CP * x) * ldb, b_voff[B_ROWS_PER_CP == 16 ? (x & 1) : 0],
+                     ldsw + st + G::CP_BYTES * x);
   };
 
-  // ---- fragment offsets.  A fragment (par, ks, i) of k-tile 2p + par: row
-  // wm*WM + 32i + lane%32 of pair stage p % 3, logical chunk 4par + 2ks +
-  // lane/32, physical chunk XOR (row >> 1) & 7 = (lane%32 >> 1) & 7.
-  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
-  const int fr = lane & 31, fh = lane >> 5;
-  int a_fo[2][2], b_fo[G::NJ > 2 ? G::NJ : 2];
+  // ---- fragments.  A fragment i of k-tile 2p + par: row wm*WM + 16i +
+  // lane%16 of pair stage p % 3, logical chunk 4par + lane/16, physical chunk
+  // XOR (row >> 1) & 7 = (lane%16 >> 1) & 7.
+  const int wm = wave / H::WAVES_N, wn = wave % H::WAVES_N;
+  const int fr = lane & 15, fg = lane >> 4;
+  int a_fo[2];
 #pragma unroll
-  for (int par = 0; par < 2; ++par)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      a_fo[par][ks] = (wm * G::WM + fr) * 128 + (((4 * par + 2 * ks + fh) ^ ((fr >> 1) & 7)) << 4);
+  for (int par = 0; par < 2; ++par) a_fo[par] = (wm * H::WM + fr) * 128 + (((4 * par + fg) ^ ((fr >> 1) & 7)) << 4);
+  int b_fo[B_NT ? 1 : NJ];
   if constexpr (B_NT) {
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) b_fo[ks] = (wn * G::WN + fr) * 64 + (((2 * ks + fh) ^ swz(fr)) << 4);
+    b_fo[0] = (wn * H::WN + fr) * 64 + ((fg ^ swz(fr)) << 4);
   } else {
-    // tr8 halves as in gemm_i8_pipe
-    const int g = lane >> 4, jj = (lane >> 1) & 7, h = lane & 1;
+    // tr8 half r of fragment j: lane 16g + 2jj + h supplies k-row 16g + 8r +
+    // jj, columns wn*WN + 16j + 8h .. +8; lane 16g + c receives column
+    // wn*WN + 16j + c, k = 16g + 8r + (0..7).  bswz16 of those k-rows depends
+    // on jj and g only.
+    const int jj = (lane >> 1) & 7, h = lane & 1;
+    const int kr = 16 * fg + jj;
 #pragma unroll
-    for (int j = 0; j < G::NJ; ++j) {
-      const int c = wn * (G::WN / 16) + 2 * j + (g & 1);
-      b_fo[j] = (16 * (g >> 1) + jj) * BN + ((c ^ bswz<BN>(jj)) << 4) + 8 * h;
+    for (int j = 0; j < NJ; ++j) {
+      const int c = wn * (H::WN / 16) + j;
+      b_fo[j] = kr * BN + ((c ^ bswz16<BN>(kr)) << 4) + 8 * h;
     }
   }
 
-  struct Frags {
-    v4i a[G::NI];
-    v4i b[G::NJ];
-    miaie_v2i lo[G::NJ], hi[G::NJ];
+  struct BFrags {
+    v4i b[NJ];
+    miaie_v2i lo[NJ], hi[NJ];
   };
-  constexpr int NREAD = G::NI + (B_NT ? 1 : 2) * G::NJ;
-  // q-th LDS read of k-step ks of k-tile kt (parity PAR) into f
-  auto read_one = [&](int kt, auto par_c, int ks, int q, Frags& f) {
-    constexpr int PAR = decltype(par_c)::value;
-    if (q < G::NI) {
-      const int8_t* s = lds + ((kt >> 1) % NA2) * G::A2_BYTES;
-      f.a[q] = *reinterpret_cast<const v4i*>(s + a_fo[PAR][ks] + 4096 * q);
+  v4i alo[HI], ahi[HI];
+  BFrags bs;
+  // A fragment i (parity par) from the pair stage at byte st of the A region
+  auto read_a = [&](uint32_t st, int par, int i) __attribute__((always_inline)) -> v4i {
+    // (the stage's byte address goes through readfirstlane so that the
+    // compiler keeps it in the base register: only 2048 i, below 2^16, is
+    // left for the instruction's offset field)
+    const uint32_t sbase = __builtin_amdgcn_readfirstlane(B_REGION + st);
+    return *reinterpret_cast<const v4i*>(lds + sbase + a_fo[par] + 2048 * i);
+  };
+  constexpr int BPF = B_NT ? 1 : 2;  // B reads per fragment
+  // read r of B fragment j from the B stage at byte st
+  auto read_b = [&](int st, int j, int r) __attribute__((always_inline)) {
+    if constexpr (B_NT) {
+      bs.b[j] = *reinterpret_cast<const v4i*>(lds + st + b_fo[0] + 1024 * j);
+    } else if (r == 0) {
+      bs.lo[j] = dev::lds_read_tr8(lds + st + b_fo[j]);
     } else {
-      const int8_t* s = bl + (kt & (STAGES - 1)) * G::B_BYTES;
-      if constexpr (B_NT) {
-        f.b[q - G::NI] = *reinterpret_cast<const v4i*>(s + b_fo[ks] + 2048 * (q - G::NI));
-      } else {
-        const int j = (q - G::NI) >> 1;
-        if (((q - G::NI) & 1) == 0)
-          f.lo[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN);
-        else
-          f.hi[j] = dev::lds_read_tr8(s + b_fo[j] + ks * 32 * BN + 8 * BN);
-      }
+      bs.hi[j] = dev::lds_read_tr8(lds + st + b_fo[j] + 8 * BN);
     }
   };
-  auto bfrag = [&](const Frags& f, int j) -> v4i {
+  auto bfrag = [&](int j) __attribute__((always_inline)) -> v4i {
     if constexpr (B_NT)
-      return f.b[j];
+      return bs.b[j];
     else
-      return v4i{f.lo[j][0], f.lo[j][1], f.hi[j][0], f.hi[j][1]};
-  };
-  // LDS reads per MFMA slot: one at 256x256 (16 slots for 12 reads; 1152
-  // against 1190 cycles per k-tile with two), two at 256x128 (8 slots for 8
-  // reads; 655 against 669 with one)
-  constexpr int RPS2 = G::NMF >= 16 ? 1 : 2;
-  constexpr int READ_SLOTS = (NREAD + RPS2 - 1) / RPS2;
-  auto read_slot = [&](int kt, auto par_c, int ks, int x, Frags& f) {
-#pragma unroll
-    for (int r = 0; r < RPS2; ++r)
-      if (RPS2 * x + r < NREAD) read_one(kt, par_c, ks, read_order<G::NI, G::NJ, B_NT>(RPS2 * x + r), f);
+      return v4i{bs.lo[j][0], bs.lo[j][1], bs.hi[j][0], bs.hi[j][1]};
   };
 
   const int rnd = shift ? 1 << (shift - 1) : 0;
   const int acc0 = (WRITE_Y && !WRITE_C) ? rnd : 0;
-  v16i acc[G::NI][G::NJ];
+  v4i acc[NI][NJ];
 #pragma unroll
-  for (int i = 0; i < G::NI; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int j = 0; j < G::NJ; ++j)
-      acc[i][j] = v16i{acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0, acc0};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = v4i{acc0, acc0, acc0, acc0};
 
-  // ---- prologue: phases -9 .. -1 in order (B tiles 0..2, the first half of
-  // B tile 3, A pairs 0 and 1, the first quarter of A pair 2), then wait for
-  // B tile 0 and A pair 0 (issued by phase -6).
+  // ---- prologue: the copies of phases -9 .. -1 in phase order
   const int KP = KT / 2;
 #pragma unroll
   for (int phi = -9; phi < 0; ++phi) {
     if ((phi & 1) != 0) {
-      const int k = (phi + 7) / 2;  // B first half
+      const int k = (phi + 7) / 2;
       if (phi >= -7 && k < KT)
 #pragma unroll
-        for (int x = 0; x < G::B_CP0; ++x) copy_b(k, x);
+        for (int x = 0; x < G::B_CP0; ++x) copy_b(b_base + k * b_kstep, k * G::B_BYTES, x);
     } else {
-      const int k = (phi + 6) / 2;  // B second half
+      const int k = (phi + 6) / 2;
       if (phi >= -6 && k < KT)
 #pragma unroll
-        for (int x = G::B_CP0; x < G::B_CP; ++x) copy_b(k, x);
+        for (int x = G::B_CP0; x < G::B_CP; ++x) copy_b(b_base + k * b_kstep, k * G::B_BYTES, x);
     }
     const int p = (phi + 9) / 4, q = (phi + 9) % 4;
     if (p < KP)
 #pragma unroll
-      for (int x = 0; x < G::QA; ++x) copy_a(p, G::QA * q + x);
+      for (int x = 0; x < G::QA; ++x) copy_a(a_base + p * 128, p * G::A2_BYTES, G::QA * q + x);
   }
   if (KT >= 6)
     dev::wait_vmcnt<dev::pair_prologue_vm(G::B_CP0, G::B_CP1, G::QA)>();
@@ -672,96 +731,185 @@ __device__ __forceinline__ void pipe2_tile(int8_t* lds, int tm, int tn, const in
   dev::barrier();
   if constexpr (TIMED) t1 = __builtin_amdgcn_s_memtime();
 
-  Frags f0, f1;
-  using P0 = std::integral_constant<int, 0>;
-  using P1 = std::integral_constant<int, 1>;
 #pragma unroll
-  for (int n = 0; n < NREAD; ++n) read_one(0, P0{}, 0, read_order<G::NI, G::NJ, B_NT>(n), f0);
-
-  // The copies of one phase: nb B copies (first_b ..) of k-tile kb and na A
-  // copies (first_a ..) of pair pa, spread evenly over the MFMA slots.
-  auto copy_slot = [&](int x, int kb, int first_b, int nb, int pa, int first_a, int na) {
+  for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int c = 0; c < nb + na; ++c)
-      if ((c * G::NMF) / (nb + na) == x) {
-        if (c < nb)
-          copy_b(kb, first_b + c);
-        else
-          copy_a(pa, first_a + c - nb);
-      }
-  };
+    for (int r = 0; r < BPF; ++r) read_b(0, j, r);
+#pragma unroll
+  for (int i = 0; i < HI; ++i) alo[i] = read_a(0, 0, i);
 
-  // Tile t (parity PAR, D tiles before the last; D >= 6 for every tile of the
-  // steady loop): phase 1 multiplies k-step 0 while the k-step-1 reads and
-  // the phase's copies go out; barrier; phase 2 multiplies k-step 1 while the
-  // phase's copies and tile t+1's k-step-0 reads go out.
-  auto tile = [&](int t, auto par_c, auto d_c) {
-    constexpr int PAR = decltype(par_c)::value, D = decltype(d_c)::value;
+  // ---- per-tile state (wave-uniform), for tile t of pair P = t / 2:
+  uint32_t sa0 = 0, sa1 = G::A2_BYTES, sa2 = 2 * G::A2_BYTES;  // stages of pairs P, P+1, P+2
+  const int8_t* a_src = a_base + 2 * 128;                       // A source of pair P+2
+  const int8_t* b_src = b_base + 3 * b_kstep;                   // B source of k-tile t+3
+  int sb_rt = 0;                                                // B stage of tile t
+
+  // Tile t (parity PAR; D tiles before the last; SB = t % 4, or -1 where only
+  // known at run time), copies in the schedule above: phase 1 sends the
+  // second half of B k-tile t+3 and a quarter of A pair P+2; phase 2 the first
+  // half of B k-tile t+4 (into tile t's stage) and a quarter of A pair P+2 (t
+  // even) or P+3 (t odd, into pair P's stage).
+  auto tile = [&](auto par_c, auto d_c, auto sb_c) __attribute__((always_inline)) {
+    constexpr int PAR = decltype(par_c)::value, D = decltype(d_c)::value, SB = decltype(sb_c)::value;
     constexpr int NB1 = D >= 3 ? G::B_CP1 : 0, NB2 = D >= 4 ? G::B_CP0 : 0;
     constexpr int NA1 = (PAR == 0 ? D >= 5 : D >= 4) ? G::QA : 0;
     constexpr int NA2_ = (PAR == 0 ? D >= 5 : D >= 6) ? G::QA : 0;
     constexpr bool NEXT = D >= 1;
     constexpr int VM = dev::pair_vm(D, G::B_CP0, G::B_CP1, G::QA);
-    // phase 1: B k-tile t+3 (second half); A pair t/2+2 quarter 1 (t even) or
-    // pair (t+3)/2 quarter 3 (t odd)
-    const int pa1 = PAR == 0 ? (t >> 1) + 2 : (t + 3) >> 1;
+    const int sbc = SB >= 0 ? SB * G::B_BYTES : sb_rt;                                   // tile t
+    const int sb1 = SB >= 0 ? ((SB + 1) & 3) * G::B_BYTES : (sb_rt + G::B_BYTES) & B_MASK;  // tile t+1
+    const int sb3 = SB >= 0 ? ((SB + 3) & 3) * G::B_BYTES : (sb_rt + 3 * G::B_BYTES) & B_MASK;  // tile t+3
     constexpr int qa1 = PAR == 0 ? 1 : 3;
 #pragma unroll
-    for (int x = 0; x < G::NMF; ++x) {
-      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
-      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
-      read_slot(t, par_c, 1, x, f1);
-      copy_slot(x, t + 3, G::B_CP0, NB1, pa1, G::QA * qa1, NA1);
+    for (int x = 0; x < PH; ++x) {
+      const int j = x / HI, i = x % HI;
+      mfma16(acc[i][j], bfrag(j), alo[i]);
+      if (x < HI) ahi[x] = read_a(sa0, PAR, HI + x);
+#pragma unroll
+      for (int c = 0; c < NB1 + NA1; ++c)
+        if ((c * PH) / (NB1 + NA1 > 0 ? NB1 + NA1 : 1) == x) {
+          if (c < NB1)
+            copy_b(b_src, sb3, G::B_CP0 + c);
+          else
+            copy_a(a_src, sa2, G::QA * qa1 + c - NB1);
+        }
       dev::sched_fence();
     }
-    if constexpr (READ_SLOTS > G::NMF) {
-#pragma unroll
-      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(t, par_c, 1, x, f1);
-    }
-    // next k-tile's data has landed (own copies, then everyone's via the
-    // barrier); after the barrier no wave reads this tile's B stage again
+    // tile t+1 has landed (own copies, then everyone's via the barrier);
+    // after the barrier no wave reads tile t's B stage or, for t odd, pair
+    // P's stage again
     dev::waitcnt<VM, 0>();
     dev::barrier();
-    // phase 2: B k-tile t+4 (first half); A pair t/2+2 quarter 2 (t even) or
-    // pair (t+5)/2 quarter 0 (t odd)
-    const int pa2 = PAR == 0 ? (t >> 1) + 2 : (t + 5) >> 1;
     constexpr int qa2 = PAR == 0 ? 2 : 0;
-    using PN = std::integral_constant<int, 1 - PAR>;
+    const int8_t* const a_src2 = PAR == 0 ? a_src : a_src + 128;
+    const uint32_t sa_cp2 = PAR == 0 ? sa2 : sa0;
+    const uint32_t sa_next = PAR == 0 ? sa0 : sa1;  // pair of tile t+1
 #pragma unroll
-    for (int x = 0; x < G::NMF; ++x) {
-      const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
-      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
-      copy_slot(x, t + 4, 0, NB2, pa2, G::QA * qa2, NA2_);
-      if constexpr (NEXT) read_slot(t + 1, PN{}, 0, x, f0);
+    for (int x = 0; x < PH; ++x) {
+      const int j = x / HI, i = x % HI;
+      mfma16(acc[HI + i][j], bfrag(j), ahi[i]);
+#pragma unroll
+      for (int c = 0; c < NB2 + NA2_; ++c)
+        if ((c * PH) / (NB2 + NA2_ > 0 ? NB2 + NA2_ : 1) == x) {
+          if (c < NB2)
+            copy_b(b_src + b_kstep, sbc, c);
+          else
+            copy_a(a_src2, sa_cp2, G::QA * qa2 + c - NB2);
+        }
+      if constexpr (NEXT) {
+        if (x < HI) alo[x] = read_a(sa_next, 1 - PAR, x);
+        if (i == HI - 1) {  // last use of tile t's B fragment j
+#pragma unroll
+          for (int r = 0; r < BPF; ++r) read_b(sb1, j, r);
+        }
+      }
       dev::sched_fence();
     }
-    if constexpr (NEXT && READ_SLOTS > G::NMF) {
-#pragma unroll
-      for (int x = G::NMF; x < READ_SLOTS; ++x) read_slot(t + 1, PN{}, 0, x, f0);
+    b_src += b_kstep;
+    sb_rt = (sb_rt + G::B_BYTES) & B_MASK;
+    if constexpr (PAR == 1) {
+      const uint32_t s = sa0;
+      sa0 = sa1;
+      sa1 = sa2;
+      sa2 = s;
+      a_src += 128;
     }
   };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
   using DS = std::integral_constant<int, 64>;  // steady state
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+  using SR = std::integral_constant<int, -1>;
+  // steady tiles 0 .. KT-7, then the last six.  (With the steady loops
+  // inside the KT >= 6 branch instead, the register allocator moves the
+  // accumulators between AGPRs and VGPRs around them.)
   int t = 0;
+  for (; t + 10 <= KT; t += 4) {  // four at a time: B stages known at compile time
+    tile(P0{}, DS{}, S0{});
+    tile(P1{}, DS{}, S1{});
+    tile(P0{}, DS{}, S2{});
+    tile(P1{}, DS{}, S3{});
+  }
   for (; t + 6 < KT; t += 2) {
-    tile(t, P0{}, DS{});
-    tile(t + 1, P1{}, DS{});
+    tile(P0{}, DS{}, SR{});
+    tile(P1{}, DS{}, SR{});
   }
   if (KT >= 6) {
-    tile(t, P0{}, std::integral_constant<int, 5>{});
-    tile(t + 1, P1{}, std::integral_constant<int, 4>{});
-    t += 2;
+    tile(P0{}, std::integral_constant<int, 5>{}, SR{});
+    tile(P1{}, std::integral_constant<int, 4>{}, SR{});
   }
   if (KT >= 4) {
-    tile(t, P0{}, std::integral_constant<int, 3>{});
-    tile(t + 1, P1{}, std::integral_constant<int, 2>{});
-    t += 2;
+    tile(P0{}, std::integral_constant<int, 3>{}, SR{});
+    tile(P1{}, std::integral_constant<int, 2>{}, SR{});
   }
-  tile(t, P0{}, std::integral_constant<int, 1>{});
-  tile(t + 1, P1{}, std::integral_constant<int, 0>{});
+  tile(P0{}, std::integral_constant<int, 1>{}, SR{});
+  tile(P1{}, std::integral_constant<int, 0>{}, SR{});
+  mfma16_drain();
   if constexpr (TIMED) t2 = __builtin_amdgcn_s_memtime();
 
-  pipe_epilogue<BM, BN, NW, YQ, WRITE_C>(acc, lds, tid, wm, wn, fr, fh, m0, n0, Y, C, ldy, ldc, shift, relu,
-                                        rnd - acc0);
+  // ---- epilogue.  acc[i][j][e]: row wm*WM + 16i + lane%16, column
+  // wn*WN + 16j + 4(lane/16) + e.
+  constexpr int WM = H::WM, WN = H::WN, THREADS = 64 * NW;
+  const int rnd_add = rnd - acc0;
+  if constexpr (WRITE_C) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int m = m0 + wm * WM + 16 * i + fr;
+        const int n = n0 + wn * WN + 16 * j + 4 * fg;
+        __builtin_nontemporal_store(acc[i][j], reinterpret_cast<v4i*>(C + (size_t)m * ldc + n));
+      }
+  }
+  if constexpr (WRITE_Y) {
+    // Y leaves in NI/2 chunks of 64 rows (blocks 2c and 2c+1 of both wave
+    // rows, all BN columns) through two LDS buffers, as in pipe_epilogue.
+    constexpr int CH = BN / 16, CR = 64, CB = CR * BN;
+    static_assert(2 * CB <= BM * BN && (CR * CH) % THREADS == 0, "two chunk buffers fit the stages");
+    auto stage_rows = [&](const auto& rq, int c, int8_t* buf) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = 2 * c + u;
+        const int ml = 32 * wm + 16 * u + fr;  // row within the chunk
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int n = wn * WN + 16 * j + 4 * fg;
+          const uint32_t packed = rq.pack4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+          const int off = ml * BN + (((n >> 4) ^ (ml & (CH - 1))) << 4) + (n & 15);
+          *reinterpret_cast<uint32_t*>(buf + off) = packed;
+        }
+      }
+    };
+    auto store_rows = [&](int c, const int8_t* buf) {
+#pragma unroll
+      for (int it = 0; it < CR * CH / THREADS; ++it) {
+        const int flat = it * THREADS + tid;
+        const int ml = flat / CH, ch = flat % CH;
+        const int m = (ml / 32) * WM + 32 * c + (ml % 32);  // row within the tile
+        const v4i v = *reinterpret_cast<const v4i*>(buf + ml * BN + ((ch ^ (ml & (CH - 1))) << 4));
+        __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + ch * 16));
+      }
+    };
+    auto run = [&](const auto& rq) {
+      __syncthreads();  // the main loop's last LDS reads are done
+#pragma unroll
+      for (int c = 0; c < NI / 2; ++c) {
+        int8_t* const buf = lds + (c & 1) * CB;
+        stage_rows(rq, c, buf);
+        __syncthreads();
+        store_rows(c, buf);
+      }
+    };
+    if constexpr (YQ == Y_HI_RELU)
+      run(RequantHi<true>{shift - 8, rnd_add});
+    else if constexpr (YQ == Y_HI)
+      run(RequantHi<false>{shift - 8, rnd_add});
+    else
+      run(Requant{shift, rnd_add, relu ? 0 : -128, 127});
+  }
   if constexpr (TIMED) {
     const unsigned long long t3 = __builtin_amdgcn_s_memtime(), r3 = __builtin_amdgcn_s_memrealtime();
     const unsigned long long rec[PROBE_WORDS] = {t0, t1, t2, t3, r0, r3};
@@ -773,7 +921,7 @@ __device__ __forceinline__ void pipe2_tile(int8_t* lds, int tm, int tn, const in
 }
 
 template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED = false>
-__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
+__global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe16(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
     int relu, unsigned long long* __restrict__ probe) {
@@ -782,11 +930,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
     t0 = __builtin_amdgcn_s_memtime();
     r0 = __builtin_amdgcn_s_memrealtime();
   }
-  __shared__ __attribute__((aligned(1024))) int8_t lds[Pipe2Geom<BM, BN, NW>::LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[PairGeom<BM, BN, NW>::LDS_BYTES];
   int tm, tn;
   dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
-  pipe2_tile<BM, BN, NW, B_NT, YQ, WRITE_C, TIMED>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift, relu,
-                                                    probe, t0, r0);
+  pipe16_tile<BM, BN, NW, B_NT, YQ, WRITE_C, TIMED>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift, relu,
+                                                     probe, t0, r0);
 }
 
 // Mixed tile widths in one launch: the first M/256 * nw workgroups take the
@@ -797,25 +945,24 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe2(
 // (the MLP's 2048 x 11008 up-projection: 344 wide tiles on 256 CUs, or 688
 // narrow ones, 2.7 rounds) the planner picks the split (plan_pipe).
 template <bool B_NT, int YQ, bool WRITE_C>
-__global__ __launch_bounds__(256, 1) void gemm_i8_pipe2_mixed(
+__global__ __launch_bounds__(256, 1) void gemm_i8_pipe16_mixed(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
     int relu, int nw) {
-  __shared__ __attribute__((aligned(1024))) int8_t lds[Pipe2Geom<256, 256, 4>::LDS_BYTES];
-  static_assert(Pipe2Geom<256, 128, 4>::LDS_BYTES <= Pipe2Geom<256, 256, 4>::LDS_BYTES, "narrow tile fits");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[PairGeom<256, 256, 4>::LDS_BYTES];
   const int TM = M / 256, nwide = TM * nw;
   const int b = blockIdx.x;
   int tm, tn;
   if (b < nwide) {
     dev::tile_coords<4>(b, TM, nw, tm, tn);
-    pipe2_tile<256, 256, 4, B_NT, YQ, WRITE_C, false>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift, relu,
-                                                       nullptr, 0, 0);
+    pipe16_tile<256, 256, 4, B_NT, YQ, WRITE_C, false>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift, relu,
+                                                        nullptr, 0, 0);
   } else {
     dev::tile_coords<4>(b - nwide, TM, (N - 256 * nw) / 128, tm, tn);
     const size_t c0 = (size_t)256 * nw;  // first column of the narrow tiles
-    pipe2_tile<256, 128, 4, B_NT, YQ, WRITE_C, false>(lds, tm, tn, A, B_NT ? B + c0 * ldb : B + c0,
-                                                       Y ? Y + c0 : nullptr, C ? C + c0 : nullptr, K, lda, ldb,
-                                                       ldy, ldc, shift, relu, nullptr, 0, 0);
+    pipe16_tile<256, 128, 4, B_NT, YQ, WRITE_C, false>(lds, tm, tn, A, B_NT ? B + c0 * ldb : B + c0,
+                                                        Y ? Y + c0 : nullptr, C ? C + c0 : nullptr, K, lda, ldb,
+                                                        ldy, ldc, shift, relu, nullptr, 0, 0);
   }
 }
 

@@ -2,7 +2,7 @@
 // (M = N = K = 4096, A and B row-major, shift 10, Y only).
 //
 // Runs the library's own kernel template (aiehlc_amd/csrc/gemm_i8_kernels.hpp,
-// gemm_i8_pipe2<256, 256, 4, NN, Y_HI, no C>) twice over: the product
+// gemm_i8_pipe16<256, 256, 4, NN, Y_HI, no C>) twice over: the product
 // instantiation, and the TIMED one, which records per wave the shader clock
 // (s_memtime) at its start, after the prologue's barrier, after the last
 // k-tile and at its end, and the 100 MHz wall clock (s_memrealtime) at its
@@ -74,11 +74,11 @@ int main() {
   hipStream_t st;
   CHECK(hipStreamCreate(&st));
   auto product = [&]() {
-    hipLaunchKernelGGL((gemm_i8_pipe2<BM, BN, NW, false, Y_HI, false, false>), dim3(WGS), dim3(64 * NW), 0, st, A, B,
+    hipLaunchKernelGGL((gemm_i8_pipe16<BM, BN, NW, false, Y_HI, false, false>), dim3(WGS), dim3(64 * NW), 0, st, A, B,
                        Y, (int32_t*)nullptr, M, N, K, K, N, N, N, SHIFT, 0, (unsigned long long*)nullptr);
   };
   auto timed = [&]() {
-    hipLaunchKernelGGL((gemm_i8_pipe2<BM, BN, NW, false, Y_HI, false, true>), dim3(WGS), dim3(64 * NW), 0, st, A, B,
+    hipLaunchKernelGGL((gemm_i8_pipe16<BM, BN, NW, false, Y_HI, false, true>), dim3(WGS), dim3(64 * NW), 0, st, A, B,
                        Y, (int32_t*)nullptr, M, N, K, K, N, N, N, SHIFT, 0, P);
   };
   hipEvent_t e0, e1;
@@ -136,7 +136,7 @@ int main() {
   const unsigned long long last_start = *std::max_element(wstart.begin(), wstart.end());
   const unsigned long long first_end = *std::min_element(wend.begin(), wend.end());
   const unsigned long long last_end = *std::max_element(wend.begin(), wend.end());
-  printf("{\"kernel\": \"gemm_i8_pipe2<256, 256, 4, NN, Y_HI>\", \"shape\": [%d, %d, %d], "
+  printf("{\"kernel\": \"gemm_i8_pipe16<256, 256, 4, NN, Y_HI>\", \"shape\": [%d, %d, %d], "
          "\"timed_output_equals_product\": %s, \"span_us\": %.2f, \"start_spread_us\": %.2f, \"end_spread_us\": %.2f, "
          "\"prologue_cycles\": [%.0f, %.0f], \"cycles_per_k_tile\": [%.0f, %.0f], \"epilogue_cycles\": [%.0f, %.0f], "
          "\"clock_ghz\": %.3f, \"per_xcd\": [",

@@ -1,6 +1,7 @@
 // mfma_ceiling — measures what the MFMA units sustain on this GPU when fed
-// from registers only (no memory traffic), for the two instructions the GEMM
-// kernels use, with constant and with random operands.  MFMA power depends on
+// from registers only (no memory traffic), for the instructions the GEMM
+// kernels use (int8 32x32x32 and 16x16x64, bf16 32x32x16), with constant and
+// with random operands.  MFMA power depends on
 // operand bit toggling and the MI355X lowers its shader clock under load, so
 // the random-operand rate is the practical ceiling for random int8 / bf16
 // GEMM inputs; the spec-sheet peak assumes the 2.4 GHz maximum clock.
@@ -19,13 +20,19 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 __device__ unsigned long long g_clk[2048];
 
-template <bool BF16, bool RANDOM>
+// KIND 0: v_mfma_i32_32x32x32_i8; 1: v_mfma_f32_32x32x16_bf16; 2: two
+// v_mfma_i32_16x16x64_i8 per slot (the same MACs as one 32x32x32), updated in
+// place as the GEMM kernel does.
+template <int KIND, bool RANDOM>
 __global__ __launch_bounds__(256, 1) void probe(int* out, int iters) {
+  constexpr bool BF16 = KIND == 1;
   v16i ai[8];
   v16f af[8];
+  v4i a16[8];
   for (int i = 0; i < 8; ++i) {
     ai[i] = v16i{0};
     af[i] = v16f{0.f};
+    a16[i] = v4i{0};
   }
   v4i ra[8], rb[8];
   for (int i = 0; i < 8; ++i)
@@ -47,17 +54,27 @@ __global__ __launch_bounds__(256, 1) void probe(int* out, int iters) {
     for (int u = 0; u < 8; ++u)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        if constexpr (BF16)
+        if constexpr (KIND == 1) {
           af[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ra[i]),
                                                          __builtin_bit_cast(v8bf, rb[(i + u) & 7]), af[i], 0, 0, 0);
-        else
+        } else if constexpr (KIND == 0) {
           ai[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ra[i], rb[(i + u) & 7], ai[i], 0, 0, 0);
+        } else {
+          asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(a16[i]) : "v"(ra[i]), "v"(rb[(i + u) & 7]));
+          asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0"
+              : "+a"(a16[(i + 4) & 7])
+              : "v"(rb[i]), "v"(ra[(i + u) & 7]));
+        }
       }
   }
+  // (the asm MFMAs' results are read below only after their latency)
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   const unsigned long long c1 = clock64(), w1 = wall_clock64();
   int s = 0;
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 8; ++i) {
     for (int e = 0; e < 16; ++e) s += ai[i][e] + (int)af[i][e];
+    for (int e = 0; e < 4; ++e) s += a16[i][e];
+  }
   out[blockIdx.x * 256 + threadIdx.x] = s;
   if (threadIdx.x == 0 && blockIdx.x < 1024) {
     g_clk[2 * blockIdx.x] = c1 - c0;
@@ -74,15 +91,16 @@ __global__ __launch_bounds__(256, 1) void probe(int* out, int iters) {
     }                                                                   \
   } while (0)
 
-template <bool BF16, bool RANDOM>
+template <int KIND, bool RANDOM>
 void run(int* out, int blocks, int iters, const char* name, bool last) {
-  hipLaunchKernelGGL((probe<BF16, RANDOM>), dim3(blocks), dim3(256), 0, 0, out, 200);  // warm up
+  constexpr bool BF16 = KIND == 1;
+  hipLaunchKernelGGL((probe<KIND, RANDOM>), dim3(blocks), dim3(256), 0, 0, out, 200);  // warm up
   CHECK(hipDeviceSynchronize());
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
   CHECK(hipEventRecord(e0));
-  hipLaunchKernelGGL((probe<BF16, RANDOM>), dim3(blocks), dim3(256), 0, 0, out, iters);
+  hipLaunchKernelGGL((probe<KIND, RANDOM>), dim3(blocks), dim3(256), 0, 0, out, iters);
   CHECK(hipEventRecord(e1));
   CHECK(hipEventSynchronize(e1));
   float ms = 0;
@@ -95,8 +113,9 @@ void run(int* out, int blocks, int iters, const char* name, bool last) {
     cyc += h[2 * b];
     wall += h[2 * b + 1];
   }
-  const double mfma_per_wave = 64.0 * iters;
-  const double ops = 2.0 * (BF16 ? 16384.0 : 32768.0) * mfma_per_wave * 4 * blocks;
+  const double slots_per_wave = 64.0 * iters;  // 32768 int8 or 16384 bf16 MACs each
+  const double mfma_per_wave = slots_per_wave * (KIND == 2 ? 2 : 1);
+  const double ops = 2.0 * (BF16 ? 16384.0 : 32768.0) * slots_per_wave * 4 * blocks;
   printf("  \"%s\": {\"tops\": %.1f, \"clock_ghz\": %.3f, \"cycles_per_mfma\": %.1f}%s\n", name,
          ops / (ms * 1e-3) / 1e12, cyc / wall * 0.1, cyc / nb / mfma_per_wave, last ? "" : ",");
 }
@@ -109,10 +128,11 @@ int main(int argc, char** argv) {
   int* out = nullptr;
   CHECK(hipMalloc(&out, (size_t)cus * 256 * sizeof(int)));
   printf("{\n");
-  run<false, false>(out, cus, iters, "i8_32x32x32_constant", false);
-  run<false, true>(out, cus, iters, "i8_32x32x32_random", false);
-  run<true, false>(out, cus, iters, "bf16_32x32x16_constant", false);
-  run<true, true>(out, cus, iters, "bf16_32x32x16_random", true);
+  run<0, false>(out, cus, iters, "i8_32x32x32_constant", false);
+  run<0, true>(out, cus, iters, "i8_32x32x32_random", false);
+  run<2, true>(out, cus, iters, "i8_16x16x64_random", false);
+  run<1, false>(out, cus, iters, "bf16_32x32x16_constant", false);
+  run<1, true>(out, cus, iters, "bf16_32x32x16_random", true);
   printf("}\n");
   CHECK(hipFree(out));
   return 0;

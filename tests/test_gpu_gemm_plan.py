@@ -225,7 +225,7 @@ def test_ragged_fallback_matches_the_oracle(ctx, M, N, K, layout, lda_pad):
         b.free()
 
 
-# Mixed launches (gemm_i8_pipe2_mixed): 256x256 tiles over the first
+# Mixed launches (gemm_i8_pipe16_mixed): 256x256 tiles over the first
 # columns, 256x128 tiles over the rest.  Planned for fewer CUs where that
 # makes small shapes choose the mix; every output mode and both B layouts,
 # bit-exact against the oracle.
