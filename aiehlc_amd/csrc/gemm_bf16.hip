@@ -1,4 +1,5 @@
-// bf16 x bf16 -> fp32 GEMM on gfx950 MFMA (v_mfma_f32_32x32x16_bf16).
+// bf16 x bf16 -> fp32 GEMM on gfx950 MFMA (v_mfma_f32_16x16x32_bf16 and
+// v_mfma_f32_32x32x16_bf16).
 //
 // The benchmark's bf16 -> fp32 path; the reference has no bf16 kernel (its
 // only float check is the elementwise square of example/other/
@@ -6,13 +7,16 @@
 //
 // Same geometry as the int8 kernel: a row of an LDS tile is 64 bytes
 // (32 bf16 of k), read as 16-byte MFMA fragments with the same XOR swizzle;
-// the row-major B operand is 16-bit-transposed in registers on its way to LDS.
-//   gemm_bf16_pair     256x256, K % 64 == 0: A staged two k-tiles at a time.
+// the row-major B operand is transposed by ds_read_b64_tr_b16 on its way out
+// of LDS.
+//   gemm_bf16_pair16   256x256, K % 64 == 0: A staged two k-tiles at a time,
+//                      v_mfma_f32_16x16x32_bf16 (a higher clock than the
+//                      32x32x16 form under the power limit).
 //   gemm_bf16_tile256  256x256x32, 4 waves x (4x4 MFMA 32x32x16), four LDS stages.
 //   gemm_bf16_tile64p  64x64x32 fallback for K % 8 == 0 and an aligned A:
 //                      vector A loads, next k-tile prefetched into registers.
 //   gemm_bf16_tile64   64x64x32 bounds-checked fallback.
-// Both 256x256 kernels write C through store_tile_f32 (whole-row stores).
+// The 256x256 kernels write C through whole-row stores staged in LDS.
 #include <type_traits>
 
 #include "gfx950_ops.hpp"
@@ -259,15 +263,16 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
   store_tile_f32(acc, lds, wave, lane, C, m0, n0, N);
 }
 
-// Pair-staged variant (K % 64 == 0): A in three LDS stages of 256 rows x 128
+// Pair-staged geometry (K % 64 == 0): A in three LDS stages of 256 rows x 128
 // bytes (two k-tiles, 64 bf16 of k), so each A copy moves whole 128-byte lines
 // instead of touching 16 lines at half use; B keeps four per-k-tile stages
 // (32 k-rows of 512 bytes, whole lines already).  160 KiB of LDS.  The copy
 // schedule is the int8 pair-staged kernel's (dev::pair_vm): B k-tile k in two
 // halves at phases 2k-7 and 2k-6, A pair p in quarters at phases 4p-9+q.
-// A pair-stage row r holds logical 16-byte chunk c at c ^ ((r >> 1) & 7), so
-// a fragment read (16 consecutive rows, one logical chunk) touches 16
-// distinct bank groups.
+// A copy x of wave w: rows 8(4x + w) + lane/8, physical chunk lane%8 of the
+// row's 128 bytes, holding logical chunk (lane%8) ^ ((row >> 1) & 7), so a
+// fragment read (16 consecutive rows, one logical chunk) touches 16 distinct
+// bank groups.  B copy i: k-rows 8i + 2w + lane/32, physical chunk lane%32.
 constexpr int NA2 = 3;
 constexpr int A2_BYTES = BM * 128;                  // one A pair stage (32 KiB)
 constexpr int A_REGION = NA2 * A2_BYTES;            // 96 KiB
@@ -277,12 +282,74 @@ constexpr int A_CP2 = A2_BYTES / 4096, QA = A_CP2 / 4;  // A copies per thread p
 constexpr int B_CP = B_BYTES / 4096, B_CP0 = (B_CP + 1) / 2, B_CP1 = B_CP - B_CP0;
 static_assert(PAIR_LDS <= 163840, "pair-staged LDS budget");
 
-__global__ __launch_bounds__(256, 1) void gemm_bf16_pair(const uint16_t* __restrict__ A,
-                                                         const uint16_t* __restrict__ B,
-                                                         float* __restrict__ C, int M, int N, int K) {
+// ------------------------------------------- pair-staged, 16x16x32 MFMA
+// The pair-staged geometry above with the multiplies on
+// v_mfma_f32_16x16x32_bf16: the same MACs per cycle as the 32x32x16 form,
+// half the accumulator bits per MAC, and under the power limit a higher clock
+// (register-only random bf16 operands: 1.86 PFLOP/s at 1.82 GHz against 1.63
+// at 1.60 GHz on the 32x32x16 form, same GPU, same run).  The k-loop follows
+// the int8 kernel gemm_i8_pipe16 (gemm_i8_kernels.hpp): each wave's 128x128
+// quarter is 8 x 8 blocks of 16 x 16, a 32-wide k-tile is one k-step, block
+// rows 0-3 are multiplied in phase 1 and 4-7 in phase 2 (column-block-major),
+// one set of fragment registers, accumulators updated in place by inline
+// MFMAs (the int8 kernel's notes on why, and the CPU check of the generated
+// assembly, apply here too).
+//
+// LDS: the four B stages first (so a B fragment read is a base register plus
+// a compile-time offset where the stage is known), then the three A pair
+// stages.  B k-row k (512 bytes) holds logical 16-byte chunk c at
+// c ^ bswz16(k), bswz16(k) = ((k & 3) << 2) | (((k >> 3) & 1) << 1): a
+// fragment half (ds_read_b64_tr_b16) has lane 16g + 4jj + q supply k-row
+// 8g + 4r + jj, 8 bytes of chunk (16 wn + 2j) + q/2, and lane 16g + c
+// receives column c of the 16-column block, k = 8g + 4r + (0..3); the 32
+// lanes of a read half (g = 0, 1) then touch 16 distinct 16-byte bank groups.
+// A fragment i: row 16i + lane%16 of the wave's rows, logical chunk lane/16 of
+// the k-tile (k = 8(lane/16) .. +8), as in the int8 kernel.
+__device__ __forceinline__ int bswz16(int k) { return ((k & 3) << 2) | (((k >> 3) & 1) << 1); }
+
+__device__ __forceinline__ void mfma16_bf16(v4f& acc, v4i a, v4i b) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// fp32 epilogue of a 256x256 tile held as acc[i][j][e] = C[m0 + wm*128 + 16i +
+// lane%16][n0 + wn*128 + 16j + 4(lane/16) + e], staged through LDS in two
+// halves of 64 rows per wave row (block rows i = 4h .. 4h+3) so that every
+// store writes one whole 1 KiB row: LDS row R = wm*64 + 16(i - 4h) + lane%16,
+// 16-byte chunk c = 32 wn + 4j + lane/16 at physical chunk c ^ (R & 15).
+__device__ __forceinline__ void store_tile16_f32(const v4f (&acc)[8][8], int8_t* lds, int wave, int lane, float* C,
+                                                 int m0, int n0, int N) {
+  const int wm = wave >> 1, wn = wave & 1, fr = lane & 15, fg = lane >> 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    dev::barrier();  // the other waves' last reads of this LDS
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int R = wm * 64 + 16 * ii + fr;
+        const int c = wn * 32 + 4 * j + fg;
+        *reinterpret_cast<v4f*>(lds + R * 1024 + ((c ^ (R & 15)) << 4)) = acc[4 * h + ii][j];
+      }
+    dev::barrier();
+#pragma unroll
+    for (int rr = 0; rr < 32; ++rr) {
+      const int R = wave * 32 + rr;
+      const v4f v = *reinterpret_cast<const v4f*>(lds + R * 1024 + ((lane ^ (R & 15)) << 4));
+      const int m = m0 + (R >> 6) * 128 + 64 * h + (R & 63);
+      __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(C + (size_t)m * N + n0 + 4 * lane));
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 1) void gemm_bf16_pair16(const uint16_t* __restrict__ A,
+                                                           const uint16_t* __restrict__ B,
+                                                           float* __restrict__ C, int M, int N, int K) {
+  constexpr int B_REGION = STAGES * B_BYTES;  // 64 KiB, first
+  constexpr int B_MASK = B_REGION - 1;
+  static_assert((B_REGION & B_MASK) == 0 && B_REGION + A_REGION == PAIR_LDS, "B stages first");
+  constexpr int NI = 8, NJ = 8, HI = 4, PH = HI * NJ;
   __shared__ __attribute__((aligned(1024))) int8_t lds[PAIR_LDS];
   const uint32_t lds0 = dev::lds_addr(lds);
-  int8_t* const bl = lds + A_REGION;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -293,174 +360,191 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair(const uint16_t* __restr
   const size_t lda = (size_t)K * 2, ldb = (size_t)N * 2;  // row pitches in bytes
   const int KT = K / BK;                                   // even
 
-  // A copy x of wave w: rows 8(4x + w) + lane/8, physical chunk lane%8 of the
-  // row's 128 bytes (logical chunk (lane%8) ^ ((row >> 1) & 7), the same for
-  // every x).  B copy i: k-rows 8i + 2w + lane/32, physical chunk lane%32.
+  // copies (B with bswz16, whose bit 1 is k-row bit 3 = the copy's parity)
   const int a_r = 8 * wave + (lane >> 3);
   const uint32_t a_voff = (uint32_t)(a_r * lda) + 16 * ((lane & 7) ^ ((a_r >> 1) & 7));
   const int8_t* const a_base = reinterpret_cast<const int8_t*>(A) + (size_t)m0 * lda;
   const int b_r = 2 * wave + (lane >> 5);
-  const uint32_t b_voff = (uint32_t)(b_r * ldb) + 16 * ((lane & 31) ^ ((b_r & 3) << 2));
+  uint32_t b_voff[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) b_voff[e] = (uint32_t)(b_r * ldb) + 16 * ((lane & 31) ^ bswz16(b_r + 8 * e));
   const int8_t* const b_base = reinterpret_cast<const int8_t*>(B) + (size_t)n0 * 2;
-  auto copy_a = [&](int p, int x) {
-    dev::gload_lds16(a_base + (size_t)p * 128 + (size_t)(32 * x) * lda, a_voff,
-                     lds0 + (p % NA2) * A2_BYTES + 1024 * wave + 4096 * x);
+  const size_t b_kstep = (size_t)BK * ldb;
+  const uint32_t ldsw = lds0 + 1024 * wave;
+  auto copy_a = [&](const int8_t* src, uint32_t st, int x) __attribute__((always_inline)) {
+    dev::gload_lds16(src + (size_t)(32 * x) * lda, a_voff, ldsw + B_REGION + st + 4096 * x);
   };
-  auto copy_b = [&](int kt, int i) {
-    dev::gload_lds16(b_base + (size_t)kt * BK * ldb + (size_t)(8 * i) * ldb, b_voff,
-                     lds0 + A_REGION + (kt & (STAGES - 1)) * B_BYTES + 1024 * wave + 4096 * i);
+  auto copy_b = [&](const int8_t* src, uint32_t st, int x) __attribute__((always_inline)) {
+    dev::gload_lds16(src + (size_t)(8 * x) * ldb, b_voff[x & 1], ldsw + st + 4096 * x);
   };
 
   const int wm = wave >> 1, wn = wave & 1;
-  const int fr = lane & 31, fh = lane >> 5;
-  int a_fo[2][2], b_fo[4];
+  const int fr = lane & 15, fg = lane >> 4;
+  int a_fo[2];
 #pragma unroll
-  for (int par = 0; par < 2; ++par)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      a_fo[par][ks] = (wm * 128 + fr) * 128 + (((4 * par + 2 * ks + fh) ^ ((fr >> 1) & 7)) << 4);
+  for (int par = 0; par < 2; ++par) a_fo[par] = (wm * 128 + fr) * 128 + (((4 * par + fg) ^ ((fr >> 1) & 7)) << 4);
+  int b_fo[NJ];
   {
-    // tr16 halves as in gemm_bf16_tile256, relative to the B stage
-    const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+    const int jj = (lane >> 2) & 3, q = lane & 3;
+    const int kr = 8 * fg + jj;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = wn * 16 + 4 * j + 2 * (g & 1) + (q >> 1);
-      b_fo[j] = (8 * (g >> 1) + jj) * 512 + ((c ^ (jj << 2)) << 4) + 8 * (q & 1);
+    for (int j = 0; j < NJ; ++j) {
+      const int c = wn * 16 + 2 * j + (q >> 1);
+      b_fo[j] = kr * 512 + ((c ^ bswz16(kr)) << 4) + 8 * (q & 1);
     }
   }
-  struct Frags {
-    v4i a[4];
-    miaie_v4s lo[4], hi[4];
+  v4i alo[HI], ahi[HI];
+  miaie_v4s blo[NJ], bhi[NJ];
+  auto read_a = [&](uint32_t st, int par, int i) __attribute__((always_inline)) -> v4i {
+    const uint32_t sbase = __builtin_amdgcn_readfirstlane(B_REGION + st);
+    return *reinterpret_cast<const v4i*>(lds + sbase + a_fo[par] + 2048 * i);
   };
-  constexpr int NREAD = 12;
-  auto read_one = [&](int kt, auto par_c, int ks, int qd, Frags& f) {
-    constexpr int PAR = decltype(par_c)::value;
-    if (qd < 4) {
-      f.a[qd] = *reinterpret_cast<const v4i*>(lds + ((kt >> 1) % NA2) * A2_BYTES + a_fo[PAR][ks] + 4096 * qd);
-    } else {
-      const int8_t* s = bl + (kt & (STAGES - 1)) * B_BYTES;
-      const int j = (qd - 4) >> 1;
-      if ((qd & 1) == 0)
-        f.lo[j] = dev::lds_read_tr16(s + b_fo[j] + ks * 8192);
-      else
-        f.hi[j] = dev::lds_read_tr16(s + b_fo[j] + ks * 8192 + 2048);
-    }
+  auto read_b = [&](int st, int j) __attribute__((always_inline)) {
+    blo[j] = dev::lds_read_tr16(lds + st + b_fo[j]);
+    bhi[j] = dev::lds_read_tr16(lds + st + b_fo[j] + 2048);
   };
-  auto bfrag = [&](const Frags& f, int j) -> v8bf {
+  auto bfrag = [&](int j) __attribute__((always_inline)) -> v4i {
     typedef short v8s __attribute__((ext_vector_type(8)));
-    const v8s v = {f.lo[j][0], f.lo[j][1], f.lo[j][2], f.lo[j][3], f.hi[j][0], f.hi[j][1], f.hi[j][2], f.hi[j][3]};
-    return __builtin_bit_cast(v8bf, v);
-  };
-  // reads two per MFMA slot in first-use order: B0 (two halves), A0, B1 .. B3, A1 .. A3
-  auto read_n = [](int n) { return n < 2 ? 4 + n : n == 2 ? 0 : n <= 8 ? 3 + n : n - 8; };
-  auto read_slot = [&](int kt, auto par_c, int ks, int x, Frags& f) {
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-      if (2 * x + r < NREAD) read_one(kt, par_c, ks, read_n(2 * x + r), f);
+    const v8s v = {blo[j][0], blo[j][1], blo[j][2], blo[j][3], bhi[j][0], bhi[j][1], bhi[j][2], bhi[j][3]};
+    return __builtin_bit_cast(v4i, v);
   };
 
-  v16f acc[4][4];
+  v4f acc[NI][NJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v16f{0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   // prologue: phases -9 .. -1 in order, then wait for B k-tile 0 and A pair 0
   const int KP = KT / 2;
 #pragma unroll
   for (int phi = -9; phi < 0; ++phi) {
     if ((phi & 1) != 0) {
-      const int kb = (phi + 7) / 2;
-      if (phi >= -7 && kb < KT)
+      const int k = (phi + 7) / 2;
+      if (phi >= -7 && k < KT)
 #pragma unroll
-        for (int x = 0; x < B_CP0; ++x) copy_b(kb, x);
+        for (int x = 0; x < B_CP0; ++x) copy_b(b_base + k * b_kstep, k * B_BYTES, x);
     } else {
-      const int kb = (phi + 6) / 2;
-      if (phi >= -6 && kb < KT)
+      const int k = (phi + 6) / 2;
+      if (phi >= -6 && k < KT)
 #pragma unroll
-        for (int x = B_CP0; x < B_CP; ++x) copy_b(kb, x);
+        for (int x = B_CP0; x < B_CP; ++x) copy_b(b_base + k * b_kstep, k * B_BYTES, x);
     }
     const int p = (phi + 9) / 4, q = (phi + 9) % 4;
     if (p < KP)
 #pragma unroll
-      for (int x = 0; x < QA; ++x) copy_a(p, QA * q + x);
+      for (int x = 0; x < QA; ++x) copy_a(a_base + p * 128, p * A2_BYTES, QA * q + x);
   }
   if (KT >= 6)
     dev::wait_vmcnt<dev::pair_prologue_vm(B_CP0, B_CP1, QA)>();
   else
     dev::wait_vmcnt<0>();
   dev::barrier();
-
-  using P0 = std::integral_constant<int, 0>;
-  using P1 = std::integral_constant<int, 1>;
-  Frags f0, f1;
 #pragma unroll
-  for (int n = 0; n < NREAD; ++n) read_one(0, P0{}, 0, read_n(n), f0);
-
-  auto copy_slot = [&](int x, int kb, int first_b, int nb, int pa, int first_a, int na) {
+  for (int j = 0; j < NJ; ++j) read_b(0, j);
 #pragma unroll
-    for (int c = 0; c < nb + na; ++c)
-      if ((c * 16) / (nb + na) == x) {
-        if (c < nb)
-          copy_b(kb, first_b + c);
-        else
-          copy_a(pa, first_a + c - nb);
-      }
-  };
-  // k-tile t (parity PAR, D k-tiles before the last; D >= 6 in the steady loop)
-  auto tile = [&](int t, auto par_c, auto d_c) {
-    constexpr int PAR = decltype(par_c)::value, D = decltype(d_c)::value;
+  for (int i = 0; i < HI; ++i) alo[i] = read_a(0, 0, i);
+
+  uint32_t sa0 = 0, sa1 = A2_BYTES, sa2 = 2 * A2_BYTES;  // stages of pairs P, P+1, P+2
+  const int8_t* a_src = a_base + 2 * 128;                 // A source of pair P+2
+  const int8_t* b_src = b_base + 3 * b_kstep;             // B source of k-tile t+3
+  int sb_rt = 0;                                          // B stage of tile t
+
+  auto tile = [&](auto par_c, auto d_c, auto sb_c) __attribute__((always_inline)) {
+    constexpr int PAR = decltype(par_c)::value, D = decltype(d_c)::value, SB = decltype(sb_c)::value;
     constexpr int NB1 = D >= 3 ? B_CP1 : 0, NB2 = D >= 4 ? B_CP0 : 0;
     constexpr int NA1 = (PAR == 0 ? D >= 5 : D >= 4) ? QA : 0;
     constexpr int NA2_ = (PAR == 0 ? D >= 5 : D >= 6) ? QA : 0;
     constexpr bool NEXT = D >= 1;
     constexpr int VM = dev::pair_vm(D, B_CP0, B_CP1, QA);
-    const int pa1 = PAR == 0 ? (t >> 1) + 2 : (t + 3) >> 1;
+    const int sbc = SB >= 0 ? SB * B_BYTES : sb_rt;
+    const int sb1 = SB >= 0 ? ((SB + 1) & 3) * B_BYTES : (sb_rt + B_BYTES) & B_MASK;
+    const int sb3 = SB >= 0 ? ((SB + 3) & 3) * B_BYTES : (sb_rt + 3 * B_BYTES) & B_MASK;
     constexpr int qa1 = PAR == 0 ? 1 : 3;
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int i = x >> 2, j = dev::snake_j<4>(x);
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f0, j), __builtin_bit_cast(v8bf, f0.a[i]),
-                                                          acc[i][j], 0, 0, 0);
-      read_slot(t, par_c, 1, x, f1);
-      copy_slot(x, t + 3, B_CP0, NB1, pa1, QA * qa1, NA1);
+    for (int x = 0; x < PH; ++x) {
+      const int j = x / HI, i = x % HI;
+      mfma16_bf16(acc[i][j], bfrag(j), alo[i]);
+      if (x < HI) ahi[x] = read_a(sa0, PAR, HI + x);
+#pragma unroll
+      for (int c = 0; c < NB1 + NA1; ++c)
+        if ((c * PH) / (NB1 + NA1 > 0 ? NB1 + NA1 : 1) == x) {
+          if (c < NB1)
+            copy_b(b_src, sb3, B_CP0 + c);
+          else
+            copy_a(a_src, sa2, QA * qa1 + c - NB1);
+        }
       dev::sched_fence();
     }
     dev::waitcnt<VM, 0>();
     dev::barrier();
-    const int pa2 = PAR == 0 ? (t >> 1) + 2 : (t + 5) >> 1;
     constexpr int qa2 = PAR == 0 ? 2 : 0;
-    using PN = std::integral_constant<int, 1 - PAR>;
+    const int8_t* const a_src2 = PAR == 0 ? a_src : a_src + 128;
+    const uint32_t sa_cp2 = PAR == 0 ? sa2 : sa0;
+    const uint32_t sa_next = PAR == 0 ? sa0 : sa1;
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int i = x >> 2, j = dev::snake_j<4>(x);
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfrag(f1, j), __builtin_bit_cast(v8bf, f1.a[i]),
-                                                          acc[i][j], 0, 0, 0);
-      copy_slot(x, t + 4, 0, NB2, pa2, QA * qa2, NA2_);
-      if constexpr (NEXT) read_slot(t + 1, PN{}, 0, x, f0);
+    for (int x = 0; x < PH; ++x) {
+      const int j = x / HI, i = x % HI;
+      mfma16_bf16(acc[HI + i][j], bfrag(j), ahi[i]);
+#pragma unroll
+      for (int c = 0; c < NB2 + NA2_; ++c)
+        if ((c * PH) / (NB2 + NA2_ > 0 ? NB2 + NA2_ : 1) == x) {
+          if (c < NB2)
+            copy_b(b_src + b_kstep, sbc, c);
+          else
+            copy_a(a_src2, sa_cp2, QA * qa2 + c - NB2);
+        }
+      if constexpr (NEXT) {
+        if (x < HI) alo[x] = read_a(sa_next, 1 - PAR, x);
+        if (i == HI - 1) read_b(sb1, j);  // after the last use of tile t's B fragment j
+      }
       dev::sched_fence();
     }
+    b_src += b_kstep;
+    sb_rt = (sb_rt + B_BYTES) & B_MASK;
+    if constexpr (PAR == 1) {
+      const uint32_t s3 = sa0;
+      sa0 = sa1;
+      sa1 = sa2;
+      sa2 = s3;
+      a_src += 128;
+    }
   };
-  using DS = std::integral_constant<int, 64>;  // steady state
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using DS = std::integral_constant<int, 64>;
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+  using SR = std::integral_constant<int, -1>;
   int t = 0;
+  for (; t + 10 <= KT; t += 4) {
+    tile(P0{}, DS{}, S0{});
+    tile(P1{}, DS{}, S1{});
+    tile(P0{}, DS{}, S2{});
+    tile(P1{}, DS{}, S3{});
+  }
   for (; t + 6 < KT; t += 2) {
-    tile(t, P0{}, DS{});
-    tile(t + 1, P1{}, DS{});
+    tile(P0{}, DS{}, SR{});
+    tile(P1{}, DS{}, SR{});
   }
   if (KT >= 6) {
-    tile(t, P0{}, std::integral_constant<int, 5>{});
-    tile(t + 1, P1{}, std::integral_constant<int, 4>{});
-    t += 2;
+    tile(P0{}, std::integral_constant<int, 5>{}, SR{});
+    tile(P1{}, std::integral_constant<int, 4>{}, SR{});
   }
   if (KT >= 4) {
-    tile(t, P0{}, std::integral_constant<int, 3>{});
-    tile(t + 1, P1{}, std::integral_constant<int, 2>{});
-    t += 2;
+    tile(P0{}, std::integral_constant<int, 3>{}, SR{});
+    tile(P1{}, std::integral_constant<int, 2>{}, SR{});
   }
-  tile(t, P0{}, std::integral_constant<int, 1>{});
-  tile(t + 1, P1{}, std::integral_constant<int, 0>{});
+  tile(P0{}, std::integral_constant<int, 1>{}, SR{});
+  tile(P1{}, std::integral_constant<int, 0>{}, SR{});
+  // the last MFMAs' results are read only after their latency
+  dev::sched_fence();
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  dev::sched_fence();
 
-  store_tile_f32(acc, lds, wave, lane, C, m0, n0, N);
+  store_tile16_f32(acc, lds, wave, lane, C, m0, n0, N);
 }
 
 __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restrict__ A,
@@ -579,8 +663,8 @@ int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float
   const bool big = M % BM == 0 && N % BN == 0 && K % BK == 0 && aligned(A, 16) && aligned(B, 16) &&
                    aligned(C, 16) && K < (1 << 24) && N < (1 << 24);
   if (big && K % (2 * BK) == 0) {
-    hipLaunchKernelGGL(gemm_bf16_pair, dim3((M / BM) * (N / BN)), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
-    return check_launch(ctx, "gemm_bf16_pair");
+    hipLaunchKernelGGL(gemm_bf16_pair16, dim3((M / BM) * (N / BN)), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
+    return check_launch(ctx, "gemm_bf16_pair16");
   }
   if (big) {
     hipLaunchKernelGGL(gemm_bf16_tile256, dim3((M / BM) * (N / BN)), dim3(256), 0, ctx->stream, A, B, C, M, N, K);

@@ -457,7 +457,7 @@ def extra_bf16(ctx, timer, args) -> dict:
     for b in (dAb, dBb, dCb):
         b.free()
     tf = 2.0 * Mb ** 3 / (ms_b * 1e-3) / 1e12
-    return {"kernel": "gemm_bf16_pair", "ms_per_step": round(ms_b, 4),
+    return {"kernel": "gemm_bf16_pair16", "ms_per_step": round(ms_b, 4),
             "tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4),
             "timed_launches": n_b, "warmup": 5,
             "how": f"{args.settle} s of untimed launches, 5 warm-ups, then {n_b} back-to-back "
