@@ -122,7 +122,9 @@ int mlp_i8_checked(miaie_ctx* ctx, const char* fn, const int8_t* X, const int8_t
   if ((rc = check_shift(ctx, fn, "s1", s1))) return rc;
   if ((rc = check_shift(ctx, fn, "s2", s2))) return rc;
   // stage 1: H = relu(rq_s1(X . W1))   (k1 of multi_tile.cpp:39-42)
-  rc = launch_gemm_i8(ctx, X, W1, H, nullptr, M, F, K, K, F, F, F, 0, s1, 1);
+  // (H is written with ordinary stores: stage 2 reads it right after, and
+  // non-temporal ones cost 4-5% of the MLP)
+  rc = launch_gemm_i8(ctx, X, W1, H, nullptr, M, F, K, K, F, F, F, 0, s1, 1, true);
   if (rc) return rc;
   // stage 2: Y = rq_s2(H . W2), queued behind stage 1 on the same stream
   // (the tile -> tile hand-off of multi_tile.cpp:125-127 without a host trip)

@@ -203,9 +203,12 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64p(const int8_t* __restrict_
   }
 }
 
+// keep_y: the caller reads Y right after (the MLP's H): ordinary stores that
+// leave it in the caches (instantiated for NN B with ReLU, the MLP's form;
+// other calls ignore it).
 template <int BM, int BN, bool B_NT>
 void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
-                 int lda, int ldb, int ldy, int ldc, int shift, int relu) {
+                 int lda, int ldb, int ldy, int ldc, int shift, int relu, bool keep_y) {
   constexpr int NW = 4;
   dim3 grid((M / BM) * (N / BN)), block(64 * NW);
   const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
@@ -220,6 +223,15 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
   // 16x16x64 MFMAs (gemm_i8_pipe16).  128x128 tiles keep gemm_i8_pipe.
   if constexpr (BM == 256) {
     if (K % 128 == 0) {
+      if constexpr (!B_NT) {
+        if (keep_y && !C && relu) {
+          if (yq == Y_HI_RELU)
+            go2(gemm_i8_pipe16<BM, BN, NW, false, Y_HI_RELU, false, false, true>);
+          else
+            go2(gemm_i8_pipe16<BM, BN, NW, false, Y_MED3, false, false, true>);
+          return;
+        }
+      }
       if (C) {
         switch (yq) {
           case Y_NONE: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_NONE, true>); break;
@@ -255,12 +267,21 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
 
 template <bool B_NT>
 void launch_pipe_mixed(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
-                       int lda, int ldb, int ldy, int ldc, int shift, int relu, int nw) {
+                       int lda, int ldb, int ldy, int ldc, int shift, int relu, int nw, bool keep_y) {
   const dim3 grid((M / 256) * (nw + (N - 256 * nw) / 128)), block(256);
   const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw);
   };
+  if constexpr (!B_NT) {
+    if (keep_y && !C && relu) {
+      if (yq == Y_HI_RELU)
+        go(gemm_i8_pipe16_mixed<false, Y_HI_RELU, false, true>);
+      else
+        go(gemm_i8_pipe16_mixed<false, Y_MED3, false, true>);
+      return;
+    }
+  }
   if (C) {
     switch (yq) {
       case Y_NONE: go(gemm_i8_pipe16_mixed<B_NT, Y_NONE, true>); break;
@@ -409,28 +430,28 @@ int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_p
 
 // Chooses the kernel.  Y and/or C may be NULL (not both).
 int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
-                   int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu) {
+                   int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu, bool keep_y) {
   miaie_gemm_plan plan;
   const bool dense_ok = pipe_operands_ok(A, B, Y, C, K, lda, ldb, ldy, ldc);
   plan_gemm_i8(ctx, M, N, K, dense_ok, &plan);
   if (plan.kernel == MIAIE_KERNEL_PIPE_MIXED) {
     const int nw = plan_pipe(M, N, K, ctx->cus).nw;
-    b_nt ? launch_pipe_mixed<true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw)
-         : launch_pipe_mixed<false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw);
+    b_nt ? launch_pipe_mixed<true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw, keep_y)
+         : launch_pipe_mixed<false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw, keep_y);
     return check_launch(ctx, "gemm_i8_pipe16_mixed");
   }
   if (plan.kernel == MIAIE_KERNEL_PIPE) {
     hipStream_t st = ctx->stream;
     const int bm = plan.tile_m, bn = plan.tile_n;
     if (bm == 256 && bn == 256)
-      b_nt ? launch_pipe<256, 256, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu)
-           : launch_pipe<256, 256, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+      b_nt ? launch_pipe<256, 256, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
+           : launch_pipe<256, 256, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
     else if (bm == 256)
-      b_nt ? launch_pipe<256, 128, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu)
-           : launch_pipe<256, 128, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+      b_nt ? launch_pipe<256, 128, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
+           : launch_pipe<256, 128, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
     else
-      b_nt ? launch_pipe<128, 128, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu)
-           : launch_pipe<128, 128, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+      b_nt ? launch_pipe<128, 128, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
+           : launch_pipe<128, 128, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
     return check_launch(ctx, "gemm_i8_pipe");
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64), block(256);

@@ -581,7 +581,9 @@ struct Pipe16Geom {
   static_assert(NI % 2 == 0 && NJ >= 1 && HI * 16 * 2 == WM, "16x16 blocks per wave");
 };
 
-template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED>
+// KEEP_Y: Y written with ordinary stores, which leave it in the caches for
+// a kernel that reads it next (the MLP's H); otherwise non-temporal.
+template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED, bool KEEP_Y = false>
 __device__ __forceinline__ void pipe16_tile(int8_t* lds, int tm, int tn, const int8_t* __restrict__ A,
                                             const int8_t* __restrict__ B, int8_t* __restrict__ Y,
                                             int32_t* __restrict__ C, int K, int lda, int ldb, int ldy, int ldc,
@@ -890,7 +892,11 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int tm, int tn, const i
         const int ml = flat / CH, ch = flat % CH;
         const int m = (ml / 32) * WM + 32 * c + (ml % 32);  // row within the tile
         const v4i v = *reinterpret_cast<const v4i*>(buf + ml * BN + ((ch ^ (ml & (CH - 1))) << 4));
-        __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + ch * 16));
+        v4i* const dst = reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + ch * 16);
+        if constexpr (KEEP_Y)
+          *dst = v;
+        else
+          __builtin_nontemporal_store(v, dst);
       }
     };
     auto run = [&](const auto& rq) {
@@ -920,7 +926,7 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int tm, int tn, const i
   }
 }
 
-template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED = false>
+template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED = false, bool KEEP_Y = false>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe16(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
@@ -933,8 +939,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe16(
   __shared__ __attribute__((aligned(1024))) int8_t lds[PairGeom<BM, BN, NW>::LDS_BYTES];
   int tm, tn;
   dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
-  pipe16_tile<BM, BN, NW, B_NT, YQ, WRITE_C, TIMED>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift, relu,
-                                                     probe, t0, r0);
+  pipe16_tile<BM, BN, NW, B_NT, YQ, WRITE_C, TIMED, KEEP_Y>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift,
+                                                             relu, probe, t0, r0);
 }
 
 // Mixed tile widths in one launch: the first M/256 * nw workgroups take the
@@ -944,7 +950,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe16(
 // free.  For shapes whose 256-wide tiles would leave most of a round empty
 // (the MLP's 2048 x 11008 up-projection: 344 wide tiles on 256 CUs, or 688
 // narrow ones, 2.7 rounds) the planner picks the split (plan_pipe).
-template <bool B_NT, int YQ, bool WRITE_C>
+template <bool B_NT, int YQ, bool WRITE_C, bool KEEP_Y = false>
 __global__ __launch_bounds__(256, 1) void gemm_i8_pipe16_mixed(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
@@ -955,12 +961,12 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe16_mixed(
   int tm, tn;
   if (b < nwide) {
     dev::tile_coords<4>(b, TM, nw, tm, tn);
-    pipe16_tile<256, 256, 4, B_NT, YQ, WRITE_C, false>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift, relu,
-                                                        nullptr, 0, 0);
+    pipe16_tile<256, 256, 4, B_NT, YQ, WRITE_C, false, KEEP_Y>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift,
+                                                                relu, nullptr, 0, 0);
   } else {
     dev::tile_coords<4>(b - nwide, TM, (N - 256 * nw) / 128, tm, tn);
     const size_t c0 = (size_t)256 * nw;  // first column of the narrow tiles
-    pipe16_tile<256, 128, 4, B_NT, YQ, WRITE_C, false>(lds, tm, tn, A, B_NT ? B + c0 * ldb : B + c0,
+    pipe16_tile<256, 128, 4, B_NT, YQ, WRITE_C, false, KEEP_Y>(lds, tm, tn, A, B_NT ? B + c0 * ldb : B + c0,
                                                         Y ? Y + c0 : nullptr, C ? C + c0 : nullptr, K, lda, ldb,
                                                         ldy, ldc, shift, relu, nullptr, 0, 0);
   }

@@ -49,8 +49,11 @@ int mlp_i8_checked(miaie_ctx* ctx, const char* fn, const int8_t* X, const int8_t
                    int8_t* Y, int M, int K, int F, int Nout, int s1, int s2);
 
 // ---- kernel launchers implemented in the kernel translation units ----
+// keep_y: Y is read by the next kernel (ordinary stores instead of
+// non-temporal ones where the kernel has that form).
 int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
-                   int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu);
+                   int N, int K, int lda, int ldb, int ldy, int ldc, int b_nt, int shift, int relu,
+                   bool keep_y = false);
 // Kernel plan for dense operands (dense_ok: the pipelined kernel's operand
 // conditions hold).
 int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_plan* plan);

@@ -30,8 +30,9 @@ KERNELS = [
     "gemm_i8_pipe16<256, 128, 4, false, Y_HI, false>",
     "gemm_i8_pipe16<256, 256, 4, false, Y_NONE, true>",
     "gemm_i8_pipe16<256, 256, 4, true, Y_MED3, true>",
+    "gemm_i8_pipe16<256, 256, 4, false, Y_HI_RELU, false, false, true>",
 ]
-MIXED = ["gemm_i8_pipe16_mixed<false, Y_HI_RELU, false>"]
+MIXED = ["gemm_i8_pipe16_mixed<false, Y_HI_RELU, false>", "gemm_i8_pipe16_mixed<false, Y_MED3, false, true>"]
 
 SRC = """
 #include "gemm_i8_kernels.hpp"
