@@ -224,7 +224,7 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
   if constexpr (BM == 256) {
     if (K % 128 == 0) {
       if constexpr (!B_NT) {
-        if (keep_y && !C && relu) {
+        if (keep_y && Y && !C && relu) {
           if (yq == Y_HI_RELU)
             go2(gemm_i8_pipe16<BM, BN, NW, false, Y_HI_RELU, false, false, true>);
           else
@@ -274,7 +274,7 @@ void launch_pipe_mixed(hipStream_t st, const int8_t* A, const int8_t* B, int8_t*
     hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw);
   };
   if constexpr (!B_NT) {
-    if (keep_y && !C && relu) {
+    if (keep_y && Y && !C && relu) {
       if (yq == Y_HI_RELU)
         go(gemm_i8_pipe16_mixed<false, Y_HI_RELU, false, true>);
       else

@@ -322,6 +322,35 @@ def test_mlp_i8(ctx, shape):
     assert np.array_equal(ctx.download(dY), Yo)
 
 
+@pytest.mark.parametrize("form,s1,s2", [("uniform", 5, 12), ("uniform", 11, 7), ("mixed", 6, 12),
+                                        ("mixed", 11, 12)])
+def test_mlp_i8_cached_h_forms(ctx, form, s1, s2):
+    """The up-projection writes H with ordinary stores (it is read right
+    after) in both requant forms (shift < 8: clamp; >= 8: high byte), from
+    the uniform 256x256 kernel and from the mixed-tile one.  Planned for one
+    CU, so that these small shapes take 256-row tiles."""
+    M, K, F, Nout = (256, 256, 512, 256) if form == "uniform" else (256, 256, 384, 256)
+    prev = ctx.plan_set_cus(1)
+    try:
+        up = ctx.plan_gemm_i8(M, F, K)
+        _say("mlp cached H", (M, K, F, Nout), form, "shifts", s1, s2, "plan", up)
+        want = mi.KERNEL_PIPE if form == "uniform" else mi.KERNEL_PIPE_MIXED
+        assert (up["kernel"], up["tile_m"], up["tile_n"]) == (want, 256, 256)
+        rng = np.random.default_rng(1000 + 10 * s1 + s2)
+        X = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+        W1 = rng.integers(-128, 128, size=(K, F), dtype=np.int8)
+        W2 = rng.integers(-128, 128, size=(F, Nout), dtype=np.int8)
+        dX, d1, d2 = ctx.upload(X), ctx.upload(W1), ctx.upload(W2)
+        dH, dY = ctx.empty((M, F), np.int8), ctx.empty((M, Nout), np.int8)
+        ctx.mlp_i8(dX, d1, d2, dH, dY, M, K, F, Nout, s1, s2)
+        ctx.wait(60_000)
+    finally:
+        assert ctx.plan_set_cus(prev) == 1
+    Yo, Ho = oracle.mlp_i8(X, W1, W2, s1, s2, want_h=True)
+    assert np.array_equal(ctx.download(dH), Ho)
+    assert np.array_equal(ctx.download(dY), Yo)
+
+
 def test_mlp_i8_config(ctx):
     """Config 5: X 2048x4096 -> W1 4096x11008 (rq 11 + ReLU) -> W2 11008x4096
     (rq 12).  H and Y compared with the oracle over every element."""
