@@ -9,6 +9,8 @@
 // (32 bf16 of k), read as 16-byte MFMA fragments with the same XOR swizzle;
 // the row-major B operand is transposed by ds_read_b64_tr_b16 on its way out
 // of LDS.
+// M and N need not be multiples of 256 (the launcher's conditions): the last
+// tile row and column are moved back to end at M and N.
 //   gemm_bf16_pair16   256x256, K % 64 == 0: A staged two k-tiles at a time,
 //                      v_mfma_f32_16x16x32_bf16 (a higher clock than the
 //                      32x32x16 form under the power limit).
@@ -103,8 +105,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   int tm, tn;
-  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  dev::tile_coords<4>(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = dev::tile_origin(tm, BM, M), n0 = dev::tile_origin(tn, BN, N);
   const size_t lda = (size_t)K * 2, ldb = (size_t)N * 2;  // row pitches in bytes
 
   // Copy i (< 4) of wave w fills 1 KiB of a stage: A rows 64i + 16w + lane/4
@@ -355,8 +357,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair16(const uint16_t* __res
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   int tm, tn;
-  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  dev::tile_coords<4>(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = dev::tile_origin(tm, BM, M), n0 = dev::tile_origin(tn, BN, N);
   const size_t lda = (size_t)K * 2, ldb = (size_t)N * 2;  // row pitches in bytes
   const int KT = K / BK;                                   // even
 
@@ -658,16 +660,22 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64p(const uint16_t* __restr
 namespace miaie {
 
 int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float* C, int M, int N, int K) {
-  // 256x256 kernel: whole tiles, 16-byte aligned operands, per-lane copy
-  // offsets of up to 64 rows in 32 bits.
-  const bool big = M % BM == 0 && N % BN == 0 && K % BK == 0 && aligned(A, 16) && aligned(B, 16) &&
-                   aligned(C, 16) && K < (1 << 24) && N < (1 << 24);
+  // 256x256 kernels: 16-byte aligned operands, per-lane copy offsets of up
+  // to 64 rows in 32 bits, and whole tiles, or else the last tile row
+  // (column) moved back over its neighbour (dev::tile_origin; N % 8 == 0
+  // keeps B and C rows on 16-byte chunks) when the tiles fill at least half
+  // the CUs (fewer, and the 64x64 kernel's wider grid is the faster one).
+  const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const bool whole = M % BM == 0 && N % BN == 0;
+  const bool overlap = M >= BM && N >= BN && N % 8 == 0 && 2 * tiles >= ctx->cus;
+  const bool big = (whole || overlap) && K % BK == 0 && aligned(A, 16) && aligned(B, 16) && aligned(C, 16) &&
+                   K < (1 << 24) && N < (1 << 24);
   if (big && K % (2 * BK) == 0) {
-    hipLaunchKernelGGL(gemm_bf16_pair16, dim3((M / BM) * (N / BN)), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
+    hipLaunchKernelGGL(gemm_bf16_pair16, dim3(tiles), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
     return check_launch(ctx, "gemm_bf16_pair16");
   }
   if (big) {
-    hipLaunchKernelGGL(gemm_bf16_tile256, dim3((M / BM) * (N / BN)), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
+    hipLaunchKernelGGL(gemm_bf16_tile256, dim3(tiles), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
     return check_launch(ctx, "gemm_bf16_tile256");
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64);

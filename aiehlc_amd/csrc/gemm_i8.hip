@@ -12,7 +12,11 @@
 //                   BD pairs of aie_control.cpp:854-875, generalised) filled
 //                   by global_load_lds_dwordx4; the row-major (NN) B operand
 //                   is transposed by ds_read_b64_tr_b8 on its way out of LDS.
-//                   XCD-aware tile order.  M % BM == N % BN == K % 64 == 0.
+//                   XCD-aware tile order.  K % 64 == 0, M >= BM, N >= BN;
+//                   a tile that does not divide M (N) has its last tile row
+//                   (column) moved back to end at M (N), overlapping the one
+//                   before it (dev::tile_origin), which needs N % 16 == 0
+//                   when BN does not divide N (16-byte column chunks).
 //   gemm_i8_pipe16  256-row tiles with K % 128 == 0: the same pipeline with A
 //                   staged two k-tiles at a time (A copies move whole cache
 //                   lines), multiplied on v_mfma_i32_16x16x64_i8, which runs
@@ -210,7 +214,7 @@ template <int BM, int BN, bool B_NT>
 void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
                  int lda, int ldb, int ldy, int ldc, int shift, int relu, bool keep_y) {
   constexpr int NW = 4;
-  dim3 grid((M / BM) * (N / BN)), block(64 * NW);
+  dim3 grid(((M + BM - 1) / BM) * ((N + BN - 1) / BN)), block(64 * NW);
   const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
@@ -268,7 +272,7 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
 template <bool B_NT>
 void launch_pipe_mixed(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
                        int lda, int ldb, int ldy, int ldc, int shift, int relu, int nw, bool keep_y) {
-  const dim3 grid((M / 256) * (nw + (N - 256 * nw) / 128)), block(256);
+  const dim3 grid(((M + 255) / 256) * (nw + (N - 256 * nw + 127) / 128)), block(256);
   const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw);
@@ -374,16 +378,21 @@ PipePlan plan_pipe(int M, int N, int K, int cus) {
       best = p;
     }
   };
+  // A tile that does not divide M or N still takes the shape: the last
+  // tile row or column overlaps its neighbour (dev::tile_origin), and is
+  // planned as a whole tile.  A moved-back column tile starts on a 16-byte
+  // chunk only when N % 16 == 0.
+  auto cols_ok = [&](int n, int bn) { return n >= bn && (n % bn == 0 || N % 16 == 0); };
   for (const TileChoice& t : kTiles) {
-    if (M % t.bm != 0 || N % t.bn != 0) continue;
-    const long tiles = (long)(M / t.bm) * (N / t.bn);
+    if (M < t.bm || !cols_ok(N, t.bn)) continue;
+    const long tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
     consider((double)((tiles + cus - 1) / cus) * t.unit * work, tiles * t.unit * work, PipePlan{t.bm, t.bn, 0});
   }
   // mixed 256x256 + 256x128 (the pair-staged kernel: K % 128 == 0)
-  if (M % 256 == 0 && N % 128 == 0 && N > 256 && K % 128 == 0) {
-    const long tm = M / 256;
-    for (int nw = 1; 256 * nw < N; ++nw) {
-      const long wide = tm * nw, narrow = tm * ((N - 256 * nw) / 128);
+  if (M >= 256 && K % 128 == 0) {
+    const long tm = (M + 255) / 256;
+    for (int nw = 1; cols_ok(N - 256 * nw, 128); ++nw) {
+      const long wide = tm * nw, narrow = tm * ((N - 256 * nw + 127) / 128);
       const double dw = kTiles[0].unit * work, dn = kTiles[1].unit * work;
       consider(list_makespan(wide, dw, narrow, dn, cus), wide * dw + narrow * dn, PipePlan{256, 256, nw});
     }
@@ -413,12 +422,12 @@ int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_p
     plan->kernel = MIAIE_KERNEL_PIPE_MIXED;
     plan->tile_m = 256;
     plan->tile_n = 256;
-    plan->workgroups = (M / 256) * (p.nw + (N - 256 * p.nw) / 128);
+    plan->workgroups = ((M + 255) / 256) * (p.nw + (N - 256 * p.nw + 127) / 128);
   } else if (p.bm) {
     plan->kernel = MIAIE_KERNEL_PIPE;
     plan->tile_m = p.bm;
     plan->tile_n = p.bn;
-    plan->workgroups = (M / p.bm) * (N / p.bn);
+    plan->workgroups = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
   } else {
     plan->kernel = MIAIE_KERNEL_TILE64;
     plan->tile_m = 64;

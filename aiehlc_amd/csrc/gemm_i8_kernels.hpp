@@ -254,8 +254,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   int tm, tn;
-  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  dev::tile_coords<4>(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = dev::tile_origin(tm, BM, M), n0 = dev::tile_origin(tn, BN, N);
   const int KT = K / BK;
 
   // ---- LDS copy assignment.  Copy i of wave w fills the 1 KiB block NW*i + w
@@ -584,7 +584,7 @@ struct Pipe16Geom {
 // KEEP_Y: Y written with ordinary stores, which leave it in the caches for
 // a kernel that reads it next (the MLP's H); otherwise non-temporal.
 template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C, bool TIMED, bool KEEP_Y = false>
-__device__ __forceinline__ void pipe16_tile(int8_t* lds, int tm, int tn, const int8_t* __restrict__ A,
+__device__ __forceinline__ void pipe16_tile(int8_t* lds, int m0, int n0, const int8_t* __restrict__ A,
                                             const int8_t* __restrict__ B, int8_t* __restrict__ Y,
                                             int32_t* __restrict__ C, int K, int lda, int ldb, int ldy, int ldc,
                                             int shift, int relu, unsigned long long* __restrict__ probe,
@@ -606,7 +606,6 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int tm, int tn, const i
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const int m0 = tm * BM, n0 = tn * BN;
   const int KT = K / BK;  // even
 
   // ---- copies.  A copy is one global_load_lds_dwordx4 from a wave-uniform
@@ -938,14 +937,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe16(
   }
   __shared__ __attribute__((aligned(1024))) int8_t lds[PairGeom<BM, BN, NW>::LDS_BYTES];
   int tm, tn;
-  dev::tile_coords<4>(blockIdx.x, M / BM, N / BN, tm, tn);
-  pipe16_tile<BM, BN, NW, B_NT, YQ, WRITE_C, TIMED, KEEP_Y>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift,
-                                                             relu, probe, t0, r0);
+  dev::tile_coords<4>(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  pipe16_tile<BM, BN, NW, B_NT, YQ, WRITE_C, TIMED, KEEP_Y>(lds, dev::tile_origin(tm, BM, M),
+                                                             dev::tile_origin(tn, BN, N), A, B, Y, C, K, lda, ldb,
+                                                             ldy, ldc, shift, relu, probe, t0, r0);
 }
 
-// Mixed tile widths in one launch: the first M/256 * nw workgroups take the
-// 256 x 256 tiles of output columns [0, 256 nw), the rest the 256 x 128
-// tiles of columns [256 nw, N).  Workgroups are dispatched in order, so the
+// Mixed tile widths in one launch: the first ceil(M/256) * nw workgroups
+// take the 256 x 256 tiles of output columns [0, 256 nw), the rest the
+// 256 x 128 tiles of columns [256 nw, N) (N - 256 nw >= 128; the last tile
+// row and the last narrow column are moved back as dev::tile_origin says).  Workgroups are dispatched in order, so the
 // narrow tiles fill the CUs the wide ones leave idle and then the CUs they
 // free.  For shapes whose 256-wide tiles would leave most of a round empty
 // (the MLP's 2048 x 11008 up-projection: 344 wide tiles on 256 CUs, or 688
@@ -956,19 +957,20 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_pipe16_mixed(
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
     int relu, int nw) {
   __shared__ __attribute__((aligned(1024))) int8_t lds[PairGeom<256, 256, 4>::LDS_BYTES];
-  const int TM = M / 256, nwide = TM * nw;
+  const int TM = (M + 255) / 256, nwide = TM * nw;
   const int b = blockIdx.x;
   int tm, tn;
   if (b < nwide) {
     dev::tile_coords<4>(b, TM, nw, tm, tn);
-    pipe16_tile<256, 256, 4, B_NT, YQ, WRITE_C, false, KEEP_Y>(lds, tm, tn, A, B, Y, C, K, lda, ldb, ldy, ldc, shift,
-                                                                relu, nullptr, 0, 0);
+    pipe16_tile<256, 256, 4, B_NT, YQ, WRITE_C, false, KEEP_Y>(lds, dev::tile_origin(tm, 256, M), 256 * tn, A, B, Y,
+                                                                C, K, lda, ldb, ldy, ldc, shift, relu, nullptr, 0, 0);
   } else {
-    dev::tile_coords<4>(b - nwide, TM, (N - 256 * nw) / 128, tm, tn);
+    const int nn = N - 256 * nw;  // columns of the narrow tiles (>= 128)
+    dev::tile_coords<4>(b - nwide, TM, (nn + 127) / 128, tm, tn);
     const size_t c0 = (size_t)256 * nw;  // first column of the narrow tiles
-    pipe16_tile<256, 128, 4, B_NT, YQ, WRITE_C, false, KEEP_Y>(lds, tm, tn, A, B_NT ? B + c0 * ldb : B + c0,
-                                                        Y ? Y + c0 : nullptr, C ? C + c0 : nullptr, K, lda, ldb,
-                                                        ldy, ldc, shift, relu, nullptr, 0, 0);
+    pipe16_tile<256, 128, 4, B_NT, YQ, WRITE_C, false, KEEP_Y>(
+        lds, dev::tile_origin(tm, 256, M), dev::tile_origin(tn, 128, nn), A, B_NT ? B + c0 * ldb : B + c0,
+        Y ? Y + c0 : nullptr, C ? C + c0 : nullptr, K, lda, ldb, ldy, ldc, shift, relu, nullptr, 0, 0);
   }
 }
 

@@ -122,5 +122,12 @@ __device__ __forceinline__ void tile_coords(int b, int TM, int TN, int& tm, int&
   tn = (logical % group_size) / gm;
 }
 
+// First row (column) of tile t along a dimension of `extent` rows cut into
+// tiles of `tile` (extent >= tile).  When the tile does not divide the
+// extent, the last tile is moved back to end at the extent: it overlaps its
+// neighbour, which computes the same exact sums for the shared rows, so both
+// write identical bytes there and no load or store needs a bound.
+__device__ __forceinline__ int tile_origin(int t, int tile, int extent) { return min(t * tile, extent - tile); }
+
 }  // namespace dev
 }  // namespace miaie

@@ -95,7 +95,9 @@ MIAIE_API int miaie_wait(miaie_ctx* ctx, int timeout_ms);
 /* ---- GEMM planning ------------------------------------------------------ */
 
 #define MIAIE_KERNEL_TILE64 0     /* bounds-checked 64x64 kernel, any shape and stride */
-#define MIAIE_KERNEL_PIPE 1       /* pipelined tile_m x tile_n kernel, 4-stage LDS DMA pipeline */
+#define MIAIE_KERNEL_PIPE 1       /* pipelined tile_m x tile_n kernel, 4-stage LDS DMA pipeline; M >= tile_m,
+                                     N >= tile_n, and N % 16 == 0 where tile_n does not divide N (the
+                                     last tile row/column overlaps the one before it) */
 #define MIAIE_KERNEL_PIPE_MIXED 2 /* pipelined kernel, 256x256 tiles over the first columns and 256x128
                                      tiles over the rest, in one launch (tile_m = tile_n = 256) */
 

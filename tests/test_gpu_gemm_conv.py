@@ -152,6 +152,34 @@ def test_gemm_bf16(ctx, shape):
     assert err <= 1e-5, err
 
 
+# M and N that 256 does not divide, on the 256x256 bf16 kernels: the last
+# tile row and column are moved back over their neighbours.  The launcher
+# takes them there when the tiles fill at least half the CUs, so the small
+# shapes plan for one CU; (4000, 2056, 128) fills the device as it is.
+@pytest.mark.parametrize("shape,cus", [((300, 264, 128), 1), ((300, 264, 96), 1), ((513, 520, 64), 1),
+                                       ((256, 1000, 192), 1), ((4000, 2056, 128), 0)])
+def test_gemm_bf16_ragged_256(ctx, shape, cus):
+    M, N, K = shape
+    _say("gemm_bf16 ragged 256x256", shape, "cus", cus)
+    A = synth.bf16_normal((M, K), 3, 1.0 / np.sqrt(K))
+    B = synth.bf16_normal((K, N), 4, 1.0 / np.sqrt(K))
+    prev = ctx.plan_set_cus(cus) if cus else None
+    try:
+        dA, dB, dC = ctx.upload(A), ctx.upload(B), ctx.empty((M, N), np.float32)
+        ctx.gemm_bf16_f32(dA, dB, dC, M, N, K)
+        ctx.wait(60_000)
+        Cg = ctx.download(dC).astype(np.float64)
+        for b in (dA, dB, dC):
+            b.free()
+    finally:
+        if cus:
+            ctx.plan_set_cus(prev)
+    R = oracle.gemm_bf16(A, B, f64=True)
+    err = np.abs(Cg - R).max() / np.abs(R).max()
+    assert err <= BF16_TOL, err
+    assert err <= 1e-5, err
+
+
 # K sweep over the 256x256 bf16 kernels: K % 64 == 0 takes the pair-staged
 # kernel (A staged two k-tiles at a time; its waits change over the last six
 # k-tiles and in the prologue below six), odd multiples of 32 the per-k-tile

@@ -171,13 +171,15 @@ def test_strided_operands(ctx, M, N, K, lda, ldb, ldc, layout):
         ctx.plan_set_cus(prev)
 
 
-# Ragged M / N (or K % 64 != 0) with K % 16 == 0 and 16-byte aligned A rows
-# take the prefetching 64x64 kernel (vector loads from clamped addresses, zeroed
-# outside the matrix); bit-exact in every output mode and both B layouts,
-# including products smaller than one tile and row pitches above the extent.
+# Shapes the pipelined kernels cannot take (M or N below the smallest tile,
+# N % 16 != 0 where no tile divides N, K % 64 != 0) with K % 16 == 0 and
+# 16-byte aligned A rows run the prefetching 64x64 kernel (vector loads from
+# clamped addresses, zeroed outside the matrix); bit-exact in every output
+# mode and both B layouts, including products smaller than one tile and row
+# pitches above the extent.
 @pytest.mark.parametrize("M,N,K,layout,lda_pad", [
-    (1000, 1008, 256, mi.B_NN, 0),
-    (300, 4000, 128, mi.B_NN, 0),
+    (1000, 1000, 256, mi.B_NN, 0),  # N % 16 == 8
+    (300, 4004, 128, mi.B_NT, 0),
     (129, 77, 64, mi.B_NN, 0),    # N not a multiple of 16: byte gathers down B's columns
     (33, 250, 192, mi.B_NT, 0),
     (2000, 100, 128, mi.B_NT, 0),
@@ -223,6 +225,58 @@ def test_ragged_fallback_matches_the_oracle(ctx, M, N, K, layout, lda_pad):
             b.free()
     for b in (dA, dB, dC):
         b.free()
+
+
+# M and N that no tile divides, on the pipelined kernels: the last tile row
+# (column) is moved back to end at M (N) and overlaps the one before it.
+# (cus, expected kernel, tile): planned for `cus` CUs (0: the device's).
+RAGGED = [
+    (1000, 1008, 256, mi.B_NN, 0, None, None),
+    (1000, 1008, 256, mi.B_NT, 0, None, None),
+    (300, 4000, 128, mi.B_NN, 0, None, None),
+    (300, 400, 256, mi.B_NN, 1, mi.KERNEL_PIPE, (256, 256)),   # pair-staged, both edges
+    (300, 400, 256, mi.B_NT, 1, mi.KERNEL_PIPE, (256, 256)),
+    (500, 304, 192, mi.B_NN, 1, mi.KERNEL_PIPE, (256, 128)),   # per-k-tile kernel (K % 128 == 64)
+    (500, 304, 192, mi.B_NT, 1, mi.KERNEL_PIPE, (256, 128)),
+    (130, 208, 256, mi.B_NN, 1, mi.KERNEL_PIPE, (128, 128)),
+    (500, 528, 256, mi.B_NN, 1, mi.KERNEL_PIPE_MIXED, (256, 256)),  # narrow part 272 columns
+    (500, 528, 256, mi.B_NT, 1, mi.KERNEL_PIPE_MIXED, (256, 256)),
+    (2048, 10992, 256, mi.B_NN, 0, mi.KERNEL_PIPE_MIXED, (256, 256)),
+]
+
+
+@pytest.mark.parametrize("M,N,K,layout,cus,kernel,tile", RAGGED)
+def test_ragged_pipelined_matches_the_oracle(ctx, M, N, K, layout, cus, kernel, tile):
+    prev = ctx.plan_set_cus(cus) if cus else None
+    try:
+        plan = ctx.plan_gemm_i8(M, N, K)
+        print(f"[case] ragged pipelined gemm {M}x{N}x{K} layout {layout} cus {cus} plan {plan}", flush=True)
+        assert plan["kernel"] in (mi.KERNEL_PIPE, mi.KERNEL_PIPE_MIXED)
+        if kernel is not None:
+            assert (plan["kernel"], (plan["tile_m"], plan["tile_n"])) == (kernel, tile), plan
+        rng = np.random.default_rng(M * 5 + N + K + layout)
+        A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+        B = rng.integers(-128, 128, size=(N, K) if layout == mi.B_NT else (K, N), dtype=np.int8)
+        dA, dB = ctx.upload(A), ctx.upload(B)
+        dC, dY, dY2, dC2, dY3 = (ctx.empty((M, N), np.int32), ctx.empty((M, N), np.int8),
+                                 ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int32), ctx.empty((M, N), np.int8))
+        ctx.gemm_i8_i32(dA, dB, dC, M, N, K, b_layout=layout)          # C only
+        ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, layout)    # Y only, shift >= 8
+        ctx.gemm_i8_rq(dA, dB, dY2, M, N, K, 11, True, dC2, layout)     # Y + C, ReLU
+        ctx.gemm_i8_rq(dA, dB, dY3, M, N, K, 5, True, None, layout)     # Y only, shift < 8, ReLU
+        ctx.wait(60_000)
+        C, Y, Y2, C2, Y3 = (ctx.download(d) for d in (dC, dY, dY2, dC2, dY3))
+        for b in (dA, dB, dC, dY, dY2, dC2, dY3):
+            b.free()
+    finally:
+        if cus:
+            ctx.plan_set_cus(prev)
+    Co = oracle.gemm_i8(A, B, b_nt=layout == mi.B_NT)
+    assert np.array_equal(C, Co)
+    assert np.array_equal(C2, Co)
+    assert np.array_equal(Y, oracle.requant(Co, 10))
+    assert np.array_equal(Y2, oracle.requant(Co, 11, relu=True))
+    assert np.array_equal(Y3, oracle.requant(Co, 5, relu=True))
 
 
 # Mixed launches (gemm_i8_pipe16_mixed): 256x256 tiles over the first
