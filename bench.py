@@ -441,6 +441,40 @@ def extra_m_shard(ctx, timer, args) -> dict:
     return shard
 
 
+def extra_ragged(ctx, timer, args) -> dict:
+    """Shapes that no tile divides (M and N of 4000): the pipelined kernels
+    with the last tile row and column moved back over their neighbours, int8
+    (Y only, shift 10) and bf16, beside the same kernels at 4096."""
+    import aiehlc_amd as mi
+
+    out = {}
+    for M, N, K in ((4000, 4000, 4096), (2000, 2000, 1024)):
+        dA, dB, dY = ctx.empty((M, K), np.int8), ctx.empty((K, N), np.int8), ctx.empty((M, N), np.int8)
+        ctx.fill_i8(dA, M * K, 1)
+        ctx.fill_i8(dB, K * N, 2)
+        fn = lambda: ctx.gemm_i8_rq(dA, dB, dY, M, N, K, 10, False, None, mi.B_NN)
+        settle(ctx, fn, min(args.settle, 0.2))
+        ms = timed(ctx, timer, fn, max(20, args.steps // 5), 5)
+        ops = 2.0 * M * N * K
+        out[f"int8_{M}x{N}x{K}"] = {"plan": ctx.plan_gemm_i8(M, N, K), "us": round(ms * 1e3, 2),
+                                    "tops": round(ops / (ms * 1e-3) / 1e12, 1)}
+        for b in (dA, dB, dY):
+            b.free()
+    M = N = 4000
+    K = 4096
+    dA, dB, dC = ctx.empty((M, K), np.uint16), ctx.empty((K, N), np.uint16), ctx.empty((M, N), np.float32)
+    ctx.copy_h2d(dA, mi.synth.bf16_normal((M, K), 1, 1.0 / np.sqrt(K)))
+    ctx.copy_h2d(dB, mi.synth.bf16_normal((K, N), 2, 1.0 / np.sqrt(K)))
+    fn = lambda: ctx.gemm_bf16_f32(dA, dB, dC, M, N, K)
+    settle(ctx, fn, min(args.settle, 0.2))
+    ms = timed(ctx, timer, fn, 20, 5)
+    out[f"bf16_{M}x{N}x{K}"] = {"kernel": "gemm_bf16_pair16", "us": round(ms * 1e3, 2),
+                                "tflops": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)}
+    for b in (dA, dB, dC):
+        b.free()
+    return out
+
+
 def extra_bf16(ctx, timer, args) -> dict:
     """Config 3: bf16 8192^3, fp32 accumulate and output."""
     import aiehlc_amd as mi
@@ -488,7 +522,7 @@ def extra_mlp(ctx, timer, args) -> dict:
             "frac_of_peak": round(mops / (ms_m * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
 
 
-EXTRAS = {"conv": extra_conv, "m_shard": extra_m_shard, "bf16": extra_bf16, "mlp": extra_mlp}
+EXTRAS = {"conv": extra_conv, "m_shard": extra_m_shard, "bf16": extra_bf16, "mlp": extra_mlp, "ragged": extra_ragged}
 
 
 def main() -> int:
@@ -553,6 +587,7 @@ def main() -> int:
         extras["gemm_i8_m_shard"] = extra_m_shard(ctx, timer, args)
         extras["gemm_bf16_8192"] = extra_bf16(ctx, timer, args)
         extras["mlp_i8"] = extra_mlp(ctx, timer, args)
+        extras["gemm_ragged"] = extra_ragged(ctx, timer, args)
     ctx.close()
     if not args.no_extras:
         extras["mfma_ceiling"] = mfma_ceiling()
