@@ -333,7 +333,8 @@ def test_conv2d_i8_config(ctx):
     assert np.array_equal(Yg, oracle.conv2d_nhwc_i8(X, Wt, sh, 1, 1))
 
 
-@pytest.mark.parametrize("shape", [(64, 64, 128, 64), (256, 256, 512, 256), (100, 70, 90, 30)])
+@pytest.mark.parametrize("shape", [(64, 64, 128, 64), (256, 256, 512, 256), (100, 70, 90, 30),
+                                   (1000, 512, 1088, 528)])  # M, F and Nout that no tile divides
 def test_mlp_i8(ctx, shape):
     M, K, F, Nout = shape
     _say("mlp", shape)

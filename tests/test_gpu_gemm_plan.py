@@ -28,6 +28,12 @@ def test_planner_choices(ctx):
     # its down-projection: exactly one round of 256x128 tiles
     down = ctx.plan_gemm_i8(2048, 4096, 11008)
     assert (down["kernel"], down["tile_m"], down["tile_n"]) == (mi.KERNEL_PIPE, 256, 128)
+    # M and N that no tile divides: the same tiles, the last row and column
+    # overlapping their neighbours (16 x 16 tiles of 256 cover 4000)
+    ragged = ctx.plan_gemm_i8(4000, 4000, 4096)
+    assert (ragged["kernel"], ragged["tile_m"], ragged["tile_n"], ragged["workgroups"]) == (mi.KERNEL_PIPE, 256, 256, 256)
+    assert ctx.plan_gemm_i8(4000, 4004, 4096)["kernel"] == mi.KERNEL_TILE64  # N % 16 != 0 and no tile divides N
+    assert ctx.plan_gemm_i8(4000, 4096, 4096)["kernel"] == mi.KERNEL_PIPE    # only M ragged: any N a tile divides
     # shapes the pipelined kernel cannot take
     assert ctx.plan_gemm_i8(100, 50, 30)["kernel"] == mi.KERNEL_TILE64
     assert ctx.plan_gemm_i8(128, 128, 100)["kernel"] == mi.KERNEL_TILE64
