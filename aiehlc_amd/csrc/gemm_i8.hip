@@ -213,7 +213,10 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64p(const int8_t* __restrict_
 template <int BM, int BN, bool B_NT>
 void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
                  int lda, int ldb, int ldy, int ldc, int shift, int relu, bool keep_y) {
-  constexpr int NW = 4;
+  // 128x128 tiles (small grids, where the power limit does not bind): two
+  // waves per SIMD, so one wave's MFMAs run while the other waits at the
+  // k-tile's barrier or for its LDS reads
+  constexpr int NW = BM == 128 ? 8 : 4;
   dim3 grid(((M + BM - 1) / BM) * ((N + BN - 1) / BN)), block(64 * NW);
   const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
   auto go = [&](auto kernel) {
@@ -417,7 +420,7 @@ static bool pipe_operands_ok(const int8_t* A, const int8_t* B, const int8_t* Y, 
 int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_plan* plan) {
   const PipePlan p = dense_ok ? plan_pipe(M, N, K, ctx->cus) : PipePlan{};
   *plan = miaie_gemm_plan{};
-  plan->threads = 256;
+  plan->threads = p.bm == 128 ? 512 : 256;
   if (p.bm && p.nw) {
     plan->kernel = MIAIE_KERNEL_PIPE_MIXED;
     plan->tile_m = 256;

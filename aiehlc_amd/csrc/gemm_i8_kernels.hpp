@@ -239,12 +239,41 @@ __device__ __forceinline__ void pipe_epilogue(v16i (&acc)[NI][NJ], int8_t* lds, 
   }
 }
 
+// s_waitcnt vmcnt((n - 1) * CP) for a run-time 1 <= n <= N, with the count
+// as the immediate it must be: the copies of all but the first of n tiles
+// (CP per tile) may stay in flight.
+template <int CP, int N>
+__device__ __forceinline__ void wait_tiles_behind(int n) {
+  if constexpr (N > 1) {
+    if (n == N)
+      dev::wait_vmcnt<(N - 1) * CP>();
+    else
+      wait_tiles_behind<CP, N - 1>(n);
+  } else {
+    dev::wait_vmcnt<0>();
+  }
+}
+
+// The last S k-tiles of an S-stage pipeline, D = KT - kt of them left when
+// tile kt runs: tile kt+S-1 (whose second half this tile issues) exists for
+// D == S, tile kt+1 for D >= 2, and the D - 2 whole tiles after kt+1 stay in
+// flight at the wait for it.  Tile(kt, PRE, MORE, NEXT, VM) as in
+// gemm_i8_pipe.
+template <int D, int S, int CP, class Tile>
+__device__ __forceinline__ void pipe_tail(Tile& tile, int& kt, int KT) {
+  if (kt == KT - D)
+    tile(kt++, std::bool_constant<D == S>{}, std::false_type{}, std::bool_constant<(D >= 2)>{},
+         std::integral_constant<int, (D >= 2 ? (D - 2) * CP : 0)>{});
+  if constexpr (D > 1) pipe_tail<D - 1, S, CP>(tile, kt, KT);
+}
+
 template <int BM, int BN, int NW, bool B_NT, int YQ, bool WRITE_C>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int8_t* __restrict__ Y,
     int32_t* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift,
     int relu) {
   using G = PipeGeom<BM, BN, NW>;
+  constexpr int S = STAGES;
   constexpr bool WRITE_Y = YQ != Y_NONE;
   __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS_BYTES];
   const uint32_t lds0 = dev::lds_addr(lds);
@@ -365,22 +394,18 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
   // the in-order wave then stalls its MFMAs behind them.
   constexpr int CP_A = (CP + 1) / 2, CP_B = CP - CP_A;
 
-  // ---- prologue: tiles 0..2 and the first half of tile 3 in flight (tile
-  // 0's phase 1 sends the second half), wait for tile 0
+  // ---- prologue: tiles 0..S-2 and the first half of tile S-1 in flight
+  // (tile 0's phase 1 sends the second half), wait for tile 0
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s)
+  for (int s = 0; s < S; ++s)
     if (s < KT) {
 #pragma unroll
-      for (int x = 0; x < (s == STAGES - 1 ? CP_A : CP); ++x) copy(s, s, x);
+      for (int x = 0; x < (s == S - 1 ? CP_A : CP); ++x) copy(s, s, x);
     }
-  if (KT >= 4)
-    dev::wait_vmcnt<2 * CP + CP_A>();
-  else if (KT == 3)
-    dev::wait_vmcnt<2 * CP>();
-  else if (KT == 2)
-    dev::wait_vmcnt<CP>();
-  else
-    dev::wait_vmcnt<0>();
+  if (KT >= S)
+    dev::wait_vmcnt<(S - 2) * CP + CP_A>();
+  else  // KT < S tiles, all issued whole: the KT - 1 after tile 0 may stay in flight
+    wait_tiles_behind<CP, S - 1>(KT);
   dev::barrier();
 
   Frags f0, f1;
@@ -402,28 +427,28 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
   };
 
   // Per tile: phase 1 multiplies k-step 0 (f0) while the reads of k-step 1
-  // (f1) and the second half of tile kt+3's copies go out between the MFMAs;
-  // then the tile barrier; phase 2 multiplies k-step 1 while the first half
-  // of tile kt+4's copies and the k-step-0 reads of tile kt+1 go out between
-  // the MFMAs.  sched_fence() pins this interleave.
-  // PRE: tile kt+3 exists (its first half went out in phase 2 of tile kt-1,
-  // or in the prologue for tile 3); MORE: tile kt+4 exists; NEXT: tile kt+1
-  // exists; VM: copies still allowed in flight once tile kt+1 has landed
-  // (those of tiles kt+2 and kt+3, the last ones issued).
+  // (f1) and the second half of tile kt+S-1's copies go out between the
+  // MFMAs; then the tile barrier; phase 2 multiplies k-step 1 while the first
+  // half of tile kt+S's copies and the k-step-0 reads of tile kt+1 go out
+  // between the MFMAs.  sched_fence() pins this interleave.
+  // PRE: tile kt+S-1 exists (its first half went out in phase 2 of tile
+  // kt-1, or in the prologue for tile S-1); MORE: tile kt+S exists; NEXT:
+  // tile kt+1 exists; VM: copies still allowed in flight once tile kt+1 has
+  // landed (those of tiles kt+2 .. kt+S-1, the last ones issued).
   auto tile = [&](int kt, auto pre_c, auto more_c, auto next_c, auto vm_c) {
     constexpr bool PRE = decltype(pre_c)::value, MORE = decltype(more_c)::value;
     constexpr bool NEXT = decltype(next_c)::value;
     constexpr int VM = decltype(vm_c)::value;
-    const int cur = kt & (STAGES - 1);
-    // stage of tile kt+3 = stage of tile kt-1, whose last reads completed
-    // before tile kt-1's barrier (for kt = 0: stage 3, not read yet)
-    const int pre_stage = (kt + 3) & (STAGES - 1);
+    const int cur = kt & (S - 1);
+    // stage of tile kt+S-1 = stage of tile kt-1, whose last reads completed
+    // before tile kt-1's barrier (for kt = 0: stage S-1, not read yet)
+    const int pre_stage = (kt + S - 1) & (S - 1);
 #pragma unroll
     for (int x = 0; x < G::NMF; ++x) {
       const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f0, j), f0.a[i], acc[i][j], 0, 0, 0);
       read_slot(cur, 1, x, f1);
-      if constexpr (PRE) copy_slot(kt + 3, pre_stage, x, CP_A, CP_B);
+      if constexpr (PRE) copy_slot(kt + S - 1, pre_stage, x, CP_A, CP_B);
       dev::sched_fence();
     }
     if constexpr (READ_SLOTS > G::NMF) {
@@ -432,15 +457,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     }
     // Tile kt+1 must have landed (own copies, then everyone's via the
     // barrier); after the barrier no wave reads stage `cur` again, so the
-    // copies of tile kt+4 may overwrite it.
+    // copies of tile kt+S may overwrite it.
     dev::waitcnt<VM, 0>();
     dev::barrier();
-    const int nxt = (kt + 1) & (STAGES - 1);
+    const int nxt = (kt + 1) & (S - 1);
 #pragma unroll
     for (int x = 0; x < G::NMF; ++x) {
       const int i = x / G::NJ, j = dev::snake_j<G::NJ>(x);
       acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfrag(f1, j), f1.a[i], acc[i][j], 0, 0, 0);
-      if constexpr (MORE) copy_slot(kt + STAGES, cur, x, 0, CP_A);
+      if constexpr (MORE) copy_slot(kt + S, cur, x, 0, CP_A);
       if constexpr (NEXT) read_slot(nxt, 0, x, f0);
       dev::sched_fence();
     }
@@ -450,16 +475,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
     }
   };
   using T_ = std::true_type;
-  using F_ = std::false_type;
-  using V2 = std::integral_constant<int, 2 * CP>;
-  using V1 = std::integral_constant<int, CP>;
-  using V0 = std::integral_constant<int, 0>;
   int kt = 0;
-  for (; kt + STAGES < KT; ++kt) tile(kt, T_{}, T_{}, T_{}, V2{});
-  if (kt == KT - 4) tile(kt++, T_{}, F_{}, T_{}, V2{});
-  if (kt == KT - 3) tile(kt++, F_{}, F_{}, T_{}, V1{});
-  if (kt == KT - 2) tile(kt++, F_{}, F_{}, T_{}, V0{});
-  tile(kt, F_{}, F_{}, F_{}, V0{});
+  for (; kt + S < KT; ++kt) tile(kt, T_{}, T_{}, T_{}, std::integral_constant<int, (S - 2) * CP>{});
+  pipe_tail<S, S, CP>(tile, kt, KT);
 
   pipe_epilogue<BM, BN, NW, YQ, WRITE_C>(acc, lds, tid, wm, wn, fr, fh, m0, n0, Y, C, ldy, ldc, shift, relu,
                                         rnd - acc0);
