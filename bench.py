@@ -609,7 +609,7 @@ def main() -> int:
 
     roofline = {
         "bound": "mfma",
-        "kernel": "gemm_i8_pipe16<256, 256, 4, NN, Y_HI> (rocprof: miaie::gemm::gemm_i8_pipe16<256, 256, 4, false, 2, false, false>)",
+        "kernel": "gemm_i8_pipe16<256, 256, 4, NN, Y_HI> (rocprof: miaie::gemm::gemm_i8_pipe16<256, 256, 4, false, 2, false, false, false>)",
         "achieved": round(tops, 2),
         "peak": PEAK_INT8_TOPS,
         "unit": "TFLOP/s",
