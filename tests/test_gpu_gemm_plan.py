@@ -154,6 +154,8 @@ def _k_sweep(ctx, M, N, K, MN, layout):
     (256, 384, 384, 400, 400, 392, mi.B_NN),   # 256x128
     (128, 256, 256, 288, 304, 260, mi.B_NT),   # 128x128
     (128, 256, 256, 260, 256, 256, mi.B_NN),   # lda % 16 != 0: fallback
+    (300, 400, 256, 320, 416, 408, mi.B_NN),   # ragged M and N, pair-staged 256x256 (overlapping last tiles)
+    (500, 304, 192, 208, 224, 312, mi.B_NT),   # ragged M and N, per-k-tile 256x128
 ])
 def test_strided_operands(ctx, M, N, K, lda, ldb, ldc, layout):
     prev = ctx.plan_set_cus(1)
