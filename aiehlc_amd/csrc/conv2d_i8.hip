@@ -15,6 +15,15 @@
 // NHWC), so no im2col buffer and no LDS staging of the operands.  The four
 // partial 64x64 int32 tiles are summed through LDS, requantized and written
 // as one contiguous 4 KiB run of NHWC output.
+//
+// Split K: when the tiles cover at most a third of the CUs (the deep layers
+// of a CNN: few output pixels, long k = 9 * Cin), each tile's k-steps are divided
+// among ksplit workgroups (grid.z), which write int32 partial sums to the
+// context's workspace; conv2d_i8_splitk_reduce adds them and requantizes.
+// The two kernels are ordered by the stream, so no atomics are involved and
+// the sums are exact in any order.
+#include <algorithm>
+
 #include "conv2d_i8_rows.hpp"
 #include "miaie_internal.hpp"
 
@@ -29,10 +38,13 @@ constexpr int PIX = 64;    // pixels per workgroup
 constexpr int COB = 64;    // output channels per workgroup
 constexpr int BATCH = 6;   // k-steps whose fragments are in flight per wave
 
+// PARTIAL: k-steps [T z / ksplit, T (z+1) / ksplit) of the tile, z =
+// blockIdx.z, summed into psum[z][pixel][channel] (int32, no requantize).
+template <bool PARTIAL>
 __global__ __launch_bounds__(256) void conv2d_i8_igemm(
     const int8_t* __restrict__ X, const int8_t* __restrict__ W, const uint8_t* __restrict__ shifts,
-    int8_t* __restrict__ Y, int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad,
-    int Ho, int Wo) {
+    int8_t* __restrict__ Y, int32_t* __restrict__ psum, int N, int H, int Wd, int Cin, int Cout, int R, int S,
+    int stride, int pad, int Ho, int Wo, int ksplit) {
   __shared__ __attribute__((aligned(16))) int32_t part[4][PIX * COB];  // 64 KiB
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -63,6 +75,8 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
 
   const int CBI = Cin / 32;
   const int T = R * S * CBI;
+  const int tb = PARTIAL ? (int)((long long)T * blockIdx.z / ksplit) : 0;
+  const int te = PARTIAL ? (int)((long long)T * (blockIdx.z + 1) / ksplit) : T;
 
   v16i acc[2][2];
 #pragma unroll
@@ -70,12 +84,12 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[a][b] = v16i{0};
 
-  for (int t0 = wave; t0 < T; t0 += 4 * BATCH) {
+  for (int t0 = tb + wave; t0 < te; t0 += 4 * BATCH) {
     v4i xf[BATCH][2], wf[BATCH][2];
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
       const int t = t0 + 4 * u;
-      if (t < T) {
+      if (t < te) {
         const int rs = t / CBI, cib = t - rs * CBI;
         const int r = rs / S, s = rs - r * S;
         const int koff = rs * Cin + cib * 32;
@@ -92,7 +106,7 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
     }
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
-      if (t0 + 4 * u < T) {
+      if (t0 + 4 * u < te) {
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -133,6 +147,13 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
     sum[4 * q + 2] = s[2];
     sum[4 * q + 3] = s[3];
   }
+  if constexpr (PARTIAL) {
+    int32_t* const dst = psum + ((size_t)blockIdx.z * P + p0 + p) * Cout + co0 + c16;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<v4i*>(dst + 4 * q) = v4i{sum[4 * q], sum[4 * q + 1], sum[4 * q + 2], sum[4 * q + 3]};
+    return;
+  }
   uint32_t out[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -145,6 +166,33 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
     out[q] = v;
   }
   *reinterpret_cast<uint4*>(Y + (size_t)(p0 + p) * Cout + co0 + c16) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// The split-K epilogue: part[z][e] summed over z < ksplit for element e =
+// pixel * Cout + channel, then the per-channel requantize.  One thread per 16
+// channels of one pixel (Cout % 64 == 0).
+__global__ __launch_bounds__(256) void conv2d_i8_splitk_reduce(const int32_t* __restrict__ part,
+                                                               const uint8_t* __restrict__ shifts,
+                                                               int8_t* __restrict__ Y, long long PC, int Cout,
+                                                               int ksplit) {
+  const long long e = ((long long)blockIdx.x * 256 + threadIdx.x) * 16;
+  if (e >= PC) return;
+  v4i s[4] = {v4i{0}, v4i{0}, v4i{0}, v4i{0}};
+  for (int z = 0; z < ksplit; ++z) {
+    const int32_t* src = part + (size_t)z * PC + e;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s[q] += *reinterpret_cast<const v4i*>(src + 4 * q);
+  }
+  const int c0 = (int)(e % Cout);
+  uint32_t out[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v |= (uint32_t)(requant1(s[q][t], shifts[c0 + 4 * q + t]) & 0xFF) << (8 * t);
+    out[q] = v;
+  }
+  *reinterpret_cast<uint4*>(Y + e) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
 // Any-shape fallback: one thread per output element.
@@ -212,6 +260,20 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
   return MIAIE_CONV_DIRECT;
 }
 
+// Workgroups per tile of the implicit-GEMM kernel (1: no split).  Split when
+// at least 3 workgroups per tile fit on the CUs (a 2-way split measured no
+// faster: the reduce kernel's launch costs what the halved k-chain saves),
+// into at most 8 and at most cus / tiles parts, each keeping at least one
+// batch of loads per wave (4 * BATCH k-steps), with the partial sums inside
+// the context's workspace.
+static int conv_ksplit(size_t tiles, int T, size_t elems, const miaie_ctx* ctx) {
+  if (tiles * 3 > (size_t)ctx->cus) return 1;
+  int ks = (int)std::min<size_t>((size_t)ctx->cus / tiles, 8);
+  ks = std::min(ks, T / (4 * BATCH));
+  while (ks > 1 && (size_t)ks * elems * sizeof(int32_t) > ctx->work_bytes) --ks;
+  return ks > 1 ? ks : 1;
+}
+
 int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y,
                      int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad) {
   const int Ho = (H + 2 * pad - R) / stride + 1;
@@ -225,9 +287,20 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
     return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
   }
   if (kernel == MIAIE_CONV_IGEMM) {
-    dim3 grid((unsigned)((P + PIX - 1) / PIX), Cout / COB);
-    hipLaunchKernelGGL(conv2d_i8_igemm, grid, dim3(256), 0, ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout,
-                       R, S, stride, pad, Ho, Wo);
+    const unsigned pxb = (unsigned)((P + PIX - 1) / PIX), chb = (unsigned)(Cout / COB);
+    const int ks = conv_ksplit((size_t)pxb * chb, R * S * (Cin / 32), P * Cout, ctx);
+    if (ks > 1) {
+      int32_t* const part = static_cast<int32_t*>(ctx->work);
+      hipLaunchKernelGGL(conv2d_i8_igemm<true>, dim3(pxb, chb, (unsigned)ks), dim3(256), 0, ctx->stream, X, W,
+                         shifts, Y, part, N, H, Wd, Cin, Cout, R, S, stride, pad, Ho, Wo, ks);
+      if (int rc = check_launch(ctx, "conv2d_i8_igemm (split K)")) return rc;
+      const long long PC = (long long)(P * Cout);
+      hipLaunchKernelGGL(conv2d_i8_splitk_reduce, dim3((unsigned)((PC / 16 + 255) / 256)), dim3(256), 0,
+                         ctx->stream, part, shifts, Y, PC, Cout, ks);
+      return check_launch(ctx, "conv2d_i8_splitk_reduce");
+    }
+    hipLaunchKernelGGL(conv2d_i8_igemm<false>, dim3(pxb, chb), dim3(256), 0, ctx->stream, X, W, shifts, Y,
+                       (int32_t*)nullptr, N, H, Wd, Cin, Cout, R, S, stride, pad, Ho, Wo, 1);
     return check_launch(ctx, "conv2d_i8_igemm");
   }
   const size_t total = P * Cout;

@@ -17,8 +17,15 @@ struct miaie_ctx {
   int cus = 256;              // compute units of the device (grid sizing of persistent kernels)
   bool recording = false;     // between miaie_graph_begin and miaie_graph_end
   void* scratch = nullptr;    // device address of this device's file-scope scratch array (noalloc.hip)
+  // Device workspace owned by this context, allocated once at init so that
+  // no entry point allocates: the conv's split-K partial sums.  Work queued
+  // on the context's one stream uses it in stream order.
+  void* work = nullptr;
+  size_t work_bytes = 0;
   char err[512] = {0};
 };
+
+constexpr size_t MIAIE_CTX_WORK_BYTES = (size_t)16 << 20;
 
 namespace miaie {
 

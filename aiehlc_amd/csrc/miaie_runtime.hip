@@ -143,6 +143,14 @@ extern "C" int miaie_init_on_stream(miaie_ctx** out, int device, void* stream) {
     delete ctx;
     return rc;
   }
+  e = hipMalloc(&ctx->work, MIAIE_CTX_WORK_BYTES);
+  if (e != hipSuccess) {
+    int rc = hip_fail(nullptr, e, "hipMalloc (context workspace)");
+    (void)hipEventDestroy(ctx->done);
+    delete ctx;
+    return rc;
+  }
+  ctx->work_bytes = MIAIE_CTX_WORK_BYTES;
   *out = ctx;
   return MIAIE_OK;
 }
@@ -154,6 +162,7 @@ extern "C" int miaie_init(miaie_ctx** out, int device) {
   hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     rc = hip_fail(nullptr, e, "hipStreamCreate");
+    (void)hipFree(ctx->work);
     (void)hipEventDestroy(ctx->done);
     delete ctx;
     *out = nullptr;
@@ -175,6 +184,7 @@ extern "C" int miaie_finish(miaie_ctx* ctx) {
   }
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) rc = MIAIE_EHIP;
+  if (ctx->work) (void)hipFree(ctx->work);
   if (ctx->done) (void)hipEventDestroy(ctx->done);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
