@@ -50,7 +50,9 @@ typedef struct miaie_ctx miaie_ctx;
 
 /* Replaces XAie_SetupConfig + XAie_CfgInitialize + XAie_PartitionInitialize
  * (example/perf/aieml_perf.cc:265-313).  Binds `device` and creates a
- * stream owned by the context. */
+ * stream owned by the context.  It also allocates the context's 16 MiB
+ * device workspace (split-K partial sums of deep convolutions), released by
+ * miaie_finish, so that no compute entry point allocates. */
 MIAIE_API int miaie_init(miaie_ctx** ctx, int device);
 
 /* As miaie_init, but launches go to the caller's hipStream_t `stream`
