@@ -10,6 +10,7 @@
 #include "../../include/miaie.h"
 
 struct miaie_ctx {
+  unsigned long long id = 0;  // unique per context in the process (a graph records its context's id)
   int device = 0;
   hipStream_t stream = nullptr;
   bool own_stream = false;

@@ -9,6 +9,7 @@
 // deadline.
 #include <time.h>
 
+#include <atomic>
 #include <cstring>
 
 #include "miaie_internal.hpp"
@@ -124,6 +125,8 @@ extern "C" int miaie_init_on_stream(miaie_ctx** out, int device, void* stream) {
                 prop.gcnArchName);
   miaie_ctx* ctx = new (std::nothrow) miaie_ctx();
   if (!ctx) return fail(nullptr, MIAIE_ENOMEM, "miaie_init: host allocation failed");
+  static std::atomic<unsigned long long> next_id{1};
+  ctx->id = next_id.fetch_add(1);
   ctx->device = device;
   ctx->cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
   if (stream) {
@@ -348,6 +351,7 @@ extern "C" int miaie_plan_set_cus(miaie_ctx* ctx, int cus, int* previous) {
 
 // ---------------------------------------------------------------- recorded chains
 struct miaie_graph {
+  unsigned long long ctx_id = 0;  // the recording context: its workspace may be baked into the graph
   int device = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -387,6 +391,7 @@ extern "C" int miaie_graph_end(miaie_ctx* ctx, miaie_graph** out) {
     (void)hipGraphDestroy(g);
     return fail(ctx, MIAIE_ENOMEM, "miaie_graph_end: host allocation failed");
   }
+  mg->ctx_id = ctx->id;
   mg->device = ctx->device;
   mg->graph = g;
   (void)hipGraphGetNodes(g, nullptr, &mg->nodes);
@@ -410,9 +415,10 @@ extern "C" int miaie_graph_launch(miaie_ctx* ctx, miaie_graph* graph) {
   if (rc) return rc;
   MIAIE_CHECK_NOT_NULL(ctx, graph);
   if (ctx->recording) return fail(ctx, MIAIE_EINVAL, "miaie_graph_launch: cannot replay into a recording");
-  if (graph->device != ctx->device)
-    return fail(ctx, MIAIE_EINVAL, "miaie_graph_launch: graph recorded on device %d, context on %d", graph->device,
-                ctx->device);
+  if (graph->ctx_id != ctx->id)
+    return fail(ctx, MIAIE_EINVAL,
+                "miaie_graph_launch: the graph was recorded on another context (it may use that context's "
+                "workspace); replay it on the context that recorded it");
   hipError_t e = hipGraphLaunch(graph->exec, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphLaunch");
   return MIAIE_OK;

@@ -153,7 +153,10 @@ MIAIE_API int miaie_plan_conv2d_i8(int N, int H, int W, int Cin, int Cout, int R
  * miaie_wait, miaie_alloc, miaie_free) return MIAIE_EINVAL and record
  * nothing.  A context created on the null stream cannot record
  * (MIAIE_EUNSUPPORTED).  miaie_graph_launch queues one replay on the
- * context's stream (asynchronous, like any launch). */
+ * context's stream (asynchronous, like any launch).  A graph replays only on
+ * the context that recorded it (another context gets MIAIE_EINVAL), before
+ * that context's miaie_finish: a recorded convolution may use the context's
+ * workspace. */
 typedef struct miaie_graph miaie_graph;
 MIAIE_API int miaie_graph_begin(miaie_ctx* ctx);
 MIAIE_API int miaie_graph_end(miaie_ctx* ctx, miaie_graph** graph);

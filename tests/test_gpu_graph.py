@@ -109,6 +109,23 @@ def test_waits_and_allocations_are_refused_while_recording(ctx):
         g.destroy()
 
 
+def test_graph_replays_only_on_its_context(ctx):
+    """A recorded chain may use its context's workspace (split-K conv), so
+    another context of the same device may not replay it."""
+    buf = ctx.empty((4096,), np.int8)
+    with ctx.record() as g:
+        ctx.fill_i8(buf, 4096, 5)
+    other = mi.Context(ctx.device)
+    try:
+        assert other.call_status("miaie_graph_launch", g.handle) == mi.MIAIE_EINVAL
+        assert "another context" in other.last_error()
+        g.launch()  # its own context replays it
+        ctx.wait(10_000)
+    finally:
+        g.destroy()
+        other.close()
+
+
 def test_graph_misuse(ctx):
     h = mi.C.c_void_p()
     assert ctx.call_status("miaie_graph_end", mi.C.byref(h)) == mi.MIAIE_EINVAL      # not recording
