@@ -181,7 +181,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
   // earlier; a whole tile's copies in one phase saturate the vector-memory
   // path and stall the in-order wave's MFMAs.  The prologue sends tiles 0..2
   // and the first half of tile 3; tile 0's phase 1 sends the rest.
-  constexpr int CP_A = CP_PER_TILE / 2, CP_B = CP_PER_TILE - CP_A;
+  constexpr int CP_A = CP_PER_TILE / 2;
+  static_assert(CP_PER_TILE == 2 * CP_A, "a tile's copies go out in two equal halves");
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < KT) {

@@ -42,7 +42,6 @@ __device__ __forceinline__ void waitcnt() {
 // Wait until at most N vector-memory operations of this wave are in flight.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() { waitcnt<N, 15>(); }
-__device__ __forceinline__ void wait_lgkmcnt0() { waitcnt<63, 0>(); }
 
 // Workgroup barrier with no implied memory waits (callers wait explicitly).
 // The empty asm statements keep the compiler from moving memory accesses
