@@ -13,12 +13,14 @@
 // Each wave then runs the whole k = (r, s, ci) reduction from LDS (one
 // v_mfma_i32_32x32x32_i8 per 32-wide k-step, fully unrolled), so there is no
 // im2col buffer and no cross-wave reduction.  The requantized int8 results
-// go through a third LDS region and leave as 16-byte stores of whole output
-// pixels' channel runs: the workgroup's ROWS x Wo x WCO block is one
-// contiguous run of Y when WCO == Cout.  (Stored straight from the
-// accumulators, each lane wrote 4-byte pieces of 8 different 64-byte pixel
-// runs, and the lines left partially written in L2 made the end of every
-// launch 0.3-0.4 us longer.)
+// go through a third LDS region: each wave writes its 32 pixels x 32
+// channels there and reads them back as 16-byte pieces, two lanes per pixel,
+// so every pixel's 32 channels leave as one 32-byte run, with an LDS wait and
+// no workgroup barrier.  (Stored straight from the accumulators, each lane
+// wrote 4-byte pieces of 8 different 64-byte pixel runs, and the lines left
+// partially written in L2 made the end of every launch 0.3-0.4 us longer.
+// A workgroup-wide store of whole ROWS x Wo x WCO runs after a barrier
+// measured 0.6% slower per launch than the per-wave store.)
 //
 // Tile order: with N a multiple of 8 the grid is (8, row blocks, N/8 *
 // channel blocks) and workgroup (x, y, z) takes image 8*(z mod N/8) + x.
@@ -64,8 +66,6 @@ struct RowsGeom {
   static constexpr int W_BYTES = WCO * WP;
   static constexpr int YP = WCO + 16;                       // LDS pitch of one staged output pixel
   static constexpr int Y_BYTES = ROWS * PB * YP;
-  static constexpr int CPP = WCO / 16;                      // 16-byte output chunks per pixel
-  static_assert(ROWS * PB * CPP == 512, "one 16-byte output chunk per thread");
   static constexpr int LDS = X_BYTES + W_BYTES + Y_BYTES;
   static constexpr int T = R * S * CIN / 32;                // 32-wide k-steps
   static_assert(LDS <= 163840, "row-block conv LDS budget (160 KiB per workgroup on gfx950)");
@@ -227,19 +227,18 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
       *reinterpret_cast<uint32_t*>(yl + 8 * g) = packed;
     }
   }
-  __syncthreads();
-  // ---- store: thread -> output pixel p of the ROWS x Wo block (row-major),
-  // 16-byte channel chunk c: consecutive threads write consecutive 16 bytes
-  // of Y (one contiguous run per pixel, and per row block when WCO == Cout)
+  // ---- store: each wave stores its own 32 pixels x 32 channels from its
+  // own part of the Y region, after an LDS wait and no workgroup barrier.
+  // Lane l: pixel 32pb + l/2, 16 channels 32wc + 16(l%2), so a pixel's WCO
+  // channels leave as whole 32-byte runs.  (Padding columns px >= Wo stay in
+  // LDS.)
   {
-    const int p = tid / G::CPP, c = tid % G::CPP;
-    int prow = 0;
-#pragma unroll
-    for (int k = 1; k < ROWS; ++k) prow += p >= k * Wo;
-    const int pcol = p - prow * Wo;
-    if (pcol < Wo && ho0 + prow < Ho) {
-      const v4i v = *reinterpret_cast<const v4i*>(ys + (prow * PB + pcol) * G::YP + 16 * c);
-      *reinterpret_cast<v4i*>(Y + (uint32_t)(((n * Ho + ho0 + prow) * Wo + pcol) * Cout + co0 + 16 * c)) = v;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+    __builtin_amdgcn_wave_barrier();
+    const int sp = 32 * pb + (lane >> 1), sh = lane & 1;
+    if (sp < Wo && ho0 + rr < Ho) {
+      const v4i v = *reinterpret_cast<const v4i*>(ys + (rr * PB + sp) * G::YP + 32 * wc + 16 * sh);
+      *reinterpret_cast<v4i*>(Y + (uint32_t)(((n * Ho + ho0 + rr) * Wo + sp) * Cout + co0 + 32 * wc + 16 * sh)) = v;
     }
   }
   if constexpr (TIMED) {
