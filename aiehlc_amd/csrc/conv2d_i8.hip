@@ -25,6 +25,7 @@
 #include <algorithm>
 
 #include "conv2d_i8_rows.hpp"
+#include "gfx950_ops.hpp"
 #include "miaie_internal.hpp"
 
 namespace {
@@ -168,6 +169,188 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
   *reinterpret_cast<uint4*>(Y + (size_t)(p0 + p) * Cout + co0 + c16) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
+// ------------------------------------------------------------ taps kernel
+// LDS-staged implicit GEMM for Cin a multiple of 128 and Cout of 64 (the
+// deep layers of a CNN, which the row-block kernel does not take).  The
+// workgroup tile is 64 output pixels x 64 output channels, as in
+// conv2d_i8_igemm, but the k loop runs over stages of one filter tap (r, s)
+// and CK = 128 input channels, and each stage's two operands (the 64
+// pixels' 128 channels at that tap, and the 64 channels' weights for it) are
+// copied into an NS-stage LDS ring by global_load_lds_dwordx4 with eight
+// lanes per 128-byte row: a copy instruction touches 8 cache lines, against
+// 32 for a fragment loaded straight into MFMA layout.  The tap position is
+// walked forward without division (a runtime division per stage cost more
+// than the copies).  At Cin = 64 (two MFMAs per wave per stage) the per-stage
+// barrier and waits outweigh this, and conv2d_i8_igemm is faster.  Positions
+// outside the image are copied from a clamped address and their X fragments
+// zeroed when read.  Each of the 4 waves owns 32 pixels x 32 channels (one
+// v_mfma_i32_32x32x32_i8 accumulator), so there is no cross-wave reduction;
+// with split K (grid.z) the tile's stages are divided among workgroups whose
+// int32 partials conv2d_i8_splitk_reduce adds.
+template <int CK>
+struct TapsGeom {
+  static_assert(CK == 128, "128 input channels per stage");
+  static constexpr int NS = 8;             // LDS stages in the ring
+  static constexpr int CPR = CK / 16;      // 16-byte chunks per staged row
+  static constexpr int OPB = 64 * CK;      // one operand (64 rows) of one stage
+  static constexpr int STAGE = 2 * OPB;    // X rows, then W rows
+  static constexpr int CPO = OPB / 4096;   // copies per thread per operand per stage (256 x 16 bytes each)
+  static constexpr int CPS = 2 * CPO;      // copies per thread per stage
+  static constexpr int KS = CK / 32;       // 32-wide k-steps per stage
+  static constexpr int YP = 48;            // epilogue: LDS pitch of one pixel's 32 output channels
+  static constexpr int LDS = NS * STAGE + 4 * 32 * YP;
+  static_assert(CPO >= 1 && LDS <= 163840, "taps kernel staging");
+  static_assert((NS - 2) * CPS <= 63, "copies in flight fit the vmcnt counter");
+};
+
+// Chunk swizzle of a staged 128-byte row: the 16 rows one half-wave
+// fragment read touches land on distinct bank groups.
+__device__ __forceinline__ int taps_swz(int row) { return (row >> 1) & 7; }
+
+template <int CK, bool PARTIAL>
+__global__ __launch_bounds__(256) void conv2d_i8_taps(
+    const int8_t* __restrict__ X, const int8_t* __restrict__ W, const uint8_t* __restrict__ shifts,
+    int8_t* __restrict__ Y, int32_t* __restrict__ psum, int N, int H, int Wd, int Cin, int Cout, int R, int S,
+    int stride, int pad, int Ho, int Wo, int ksplit) {
+  using G = TapsGeom<CK>;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS];
+  const uint32_t lds0 = miaie::dev::lds_addr(lds);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 31, fh = lane >> 5;
+  const int pb = wave & 1, cb = wave >> 1;  // this wave's 32 pixels and 32 channels
+  const int P = N * Ho * Wo;
+  const int p0 = blockIdx.x * 64, co0 = blockIdx.y * 64;
+  const int CB = Cin / CK, T = R * S * CB;
+  const int sb = PARTIAL ? (int)((long long)T * blockIdx.z / ksplit) : 0;
+  const int nst = (PARTIAL ? (int)((long long)T * (blockIdx.z + 1) / ksplit) : T) - sb;
+  const int KW = R * S * Cin;
+
+  // ---- copy geometry.  Copy i (< CPO) of wave w moves 1 KiB block q = 4i + w
+  // of an operand: rows q * (1024 / CK) + lane / CPR, logical chunk
+  // (lane % CPR) ^ swz(row), landing at LDS byte q * 1024 + 16 * lane.
+  int xhb[G::CPO], xwb[G::CPO];
+  uint32_t xbase[G::CPO], wbase[G::CPO];
+  const uint32_t rowx = (uint32_t)Wd * Cin;  // bytes per input row
+#pragma unroll
+  for (int i = 0; i < G::CPO; ++i) {
+    const int row = (4 * i + wave) * (1024 / CK) + lane / G::CPR;
+    const int gc = (lane % G::CPR) ^ taps_swz(row);
+    const int p = min(p0 + row, P - 1);  // rows past the last pixel copy a real one (never stored)
+    const int wo = p % Wo, t = p / Wo;
+    xhb[i] = (t % Ho) * stride - pad;
+    xwb[i] = wo * stride - pad;
+    xbase[i] = (uint32_t)((t / Ho) * H) * rowx + (uint32_t)(16 * gc);
+    wbase[i] = (uint32_t)((co0 + row) * KW + 16 * gc);
+  }
+  // this lane's fragment pixel (X rows 32pb + fr)
+  const int pf = p0 + 32 * pb + fr;
+  const bool pvalid = pf < P;
+  int fhb, fwb;
+  {
+    const int pp = pvalid ? pf : 0;
+    const int wo = pp % Wo, t = pp / Wo;
+    fhb = (t % Ho) * stride - pad;
+    fwb = wo * stride - pad;
+  }
+
+  // A stage position (filter row r, column s, channel chunk c) walked
+  // forward without division.
+  struct Tap {
+    int r, s, c;
+  };
+  auto step = [&](Tap& t) {
+    if (++t.c == CB) {
+      t.c = 0;
+      if (++t.s == S) {
+        t.s = 0;
+        ++t.r;
+      }
+    }
+  };
+  Tap at_issue, at_use;
+  {
+    const int rs = sb / CB;
+    at_issue = Tap{rs / S, rs % S, sb % CB};
+    at_use = at_issue;
+  }
+  // copies of the stage at `t` into ring slot `slot`
+  auto issue = [&](const Tap& t, int slot) {
+    const uint32_t base = lds0 + slot * G::STAGE + 1024 * wave;
+    const uint32_t wk = (uint32_t)((t.r * S + t.s) * Cin + t.c * CK), xk = (uint32_t)(t.c * CK);
+#pragma unroll
+    for (int i = 0; i < G::CPO; ++i) {
+      const int hi = min(max(xhb[i] + t.r, 0), H - 1), wi = min(max(xwb[i] + t.s, 0), Wd - 1);
+      const uint32_t xoff = xbase[i] + (uint32_t)hi * rowx + (uint32_t)wi * Cin + xk;
+      miaie::dev::gload_lds16(X, xoff, base + 4096 * i);
+      miaie::dev::gload_lds16(W, wbase[i] + wk, base + G::OPB + 4096 * i);
+    }
+  };
+
+  v16i acc = v16i{0};
+  const int8_t* const wfrag = lds + G::OPB + (32 * cb + fr) * CK;
+  const int8_t* const xfrag = lds + (32 * pb + fr) * CK;
+  const int wsw = taps_swz(32 * cb + fr), xsw = taps_swz(32 * pb + fr);
+
+#pragma unroll
+  for (int i = 0; i < G::NS - 1; ++i)
+    if (i < nst) {
+      issue(at_issue, i);
+      step(at_issue);
+    }
+  for (int s = 0; s < nst; ++s) {
+    // this wave's copies of stage s have landed once only the stages issued
+    // after it (at most NS - 2) are in flight; the barrier publishes everyone's
+    // and frees the slot of stage s - 1 for stage s + NS - 1
+    miaie::dev::wait_tiles_behind<G::CPS, G::NS - 1>(min(G::NS - 2, nst - 1 - s) + 1);
+    miaie::dev::barrier();
+    if (s + G::NS - 1 < nst) {
+      issue(at_issue, (s + G::NS - 1) % G::NS);
+      step(at_issue);
+    }
+    const bool xin = pvalid && (unsigned)(fhb + at_use.r) < (unsigned)H && (unsigned)(fwb + at_use.s) < (unsigned)Wd;
+    step(at_use);
+    const int slot = (s % G::NS) * G::STAGE;
+#pragma unroll
+    for (int ks = 0; ks < G::KS; ++ks) {
+      const v4i wf = *reinterpret_cast<const v4i*>(wfrag + slot + (((2 * ks + fh) ^ wsw) << 4));
+      v4i xf = *reinterpret_cast<const v4i*>(xfrag + slot + (((2 * ks + fh) ^ xsw) << 4));
+      xf = xin ? xf : v4i{0};
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, xf, acc, 0, 0, 0);
+    }
+  }
+
+  // acc[4g + t]: channel 32cb + 8g + 4fh + t, pixel pf
+  const int cq = co0 + 32 * cb + 4 * fh;
+  if constexpr (PARTIAL) {
+    if (pvalid) {
+      int32_t* const dst = psum + ((size_t)blockIdx.z * P + pf) * Cout + cq;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<v4i*>(dst + 8 * g) = v4i{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+    }
+    return;
+  }
+  // requantize into this wave's own LDS block, then 16-byte stores, two
+  // lanes per pixel's 32 channels (an LDS wait, no workgroup barrier)
+  int8_t* const yb = lds + G::NS * G::STAGE + wave * 32 * G::YP;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t sh = *reinterpret_cast<const uint32_t*>(shifts + cq + 8 * g);
+    uint32_t v = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v |= (uint32_t)(requant1(acc[4 * g + t], (sh >> (8 * t)) & 0xFF) & 0xFF) << (8 * t);
+    *reinterpret_cast<uint32_t*>(yb + fr * G::YP + 8 * g + 4 * fh) = v;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+  __builtin_amdgcn_wave_barrier();
+  const int sp = lane >> 1, sh = lane & 1;
+  if (p0 + 32 * pb + sp < P) {
+    const v4i v = *reinterpret_cast<const v4i*>(yb + sp * G::YP + 16 * sh);
+    *reinterpret_cast<v4i*>(Y + (size_t)(p0 + 32 * pb + sp) * Cout + co0 + 32 * cb + 16 * sh) = v;
+  }
+}
+
 // The split-K epilogue: part[z][e] summed over z < ksplit for element e =
 // pixel * Cout + channel, then the per-channel requantize.  One thread per 16
 // channels of one pixel (Cout % 64 == 0).
@@ -254,6 +437,12 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
                        (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31) &&
                        (size_t)Cout * R * S * Cin < ((size_t)1 << 31) && Cout / 32 <= 65535;
   if (rows_ok) return MIAIE_CONV_ROWS;
+  // LDS-staged taps kernel (Cin a multiple of 128, Cout of 64): 32-bit copy
+  // offsets, so X and W each stay below 2^31 bytes; 4-byte shift loads.
+  const bool taps_ok = Cin % 128 == 0 && Cout % 64 == 0 && aligned16 && shifts_aligned4 &&
+                       (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)Cout * R * S * Cin < ((size_t)1 << 31) &&
+                       P < ((size_t)1 << 31) && Cout / 64 <= 65535;
+  if (taps_ok) return MIAIE_CONV_TAPS;
   const bool fast = Cin % 32 == 0 && Cout % COB == 0 && aligned16 && P < ((size_t)1 << 31) &&
                     (P + PIX - 1) / PIX < ((size_t)1 << 31) && Cout / COB <= 65535;
   if (fast) return MIAIE_CONV_IGEMM;
@@ -266,10 +455,10 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
 // into at most 8 and at most cus / tiles parts, each keeping at least one
 // batch of loads per wave (4 * BATCH k-steps), with the partial sums inside
 // the context's workspace.
-static int conv_ksplit(size_t tiles, int T, size_t elems, const miaie_ctx* ctx) {
+static int conv_ksplit(size_t tiles, int T, int min_per_split, size_t elems, const miaie_ctx* ctx) {
   if (tiles * 3 > (size_t)ctx->cus) return 1;
   int ks = (int)std::min<size_t>((size_t)ctx->cus / tiles, 8);
-  ks = std::min(ks, T / (4 * BATCH));
+  ks = std::min(ks, T / min_per_split);
   while (ks > 1 && (size_t)ks * elems * sizeof(int32_t) > ctx->work_bytes) --ks;
   return ks > 1 ? ks : 1;
 }
@@ -286,9 +475,28 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
     if (Cin == 64) return launch_rows<64>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
     return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
   }
+  if (kernel == MIAIE_CONV_TAPS) {
+    const unsigned pxb = (unsigned)((P + 63) / 64), chb = (unsigned)(Cout / 64);
+    const int ks = conv_ksplit((size_t)pxb * chb, R * S * (Cin / 128), 4, P * Cout, ctx);
+    auto go = [&](auto kernel, unsigned z, int32_t* psum) {
+      hipLaunchKernelGGL(kernel, dim3(pxb, chb, z), dim3(256), 0, ctx->stream, X, W, shifts, Y, psum, N, H, Wd, Cin,
+                         Cout, R, S, stride, pad, Ho, Wo, (int)z);
+    };
+    if (ks > 1) {
+      int32_t* const psum = static_cast<int32_t*>(ctx->work);
+      go(conv2d_i8_taps<128, true>, (unsigned)ks, psum);
+      if (int rc = check_launch(ctx, "conv2d_i8_taps (split K)")) return rc;
+      const long long PC = (long long)(P * Cout);
+      hipLaunchKernelGGL(conv2d_i8_splitk_reduce, dim3((unsigned)((PC / 16 + 255) / 256)), dim3(256), 0,
+                         ctx->stream, psum, shifts, Y, PC, Cout, ks);
+      return check_launch(ctx, "conv2d_i8_splitk_reduce");
+    }
+    go(conv2d_i8_taps<128, false>, 1u, nullptr);
+    return check_launch(ctx, "conv2d_i8_taps");
+  }
   if (kernel == MIAIE_CONV_IGEMM) {
     const unsigned pxb = (unsigned)((P + PIX - 1) / PIX), chb = (unsigned)(Cout / COB);
-    const int ks = conv_ksplit((size_t)pxb * chb, R * S * (Cin / 32), P * Cout, ctx);
+    const int ks = conv_ksplit((size_t)pxb * chb, R * S * (Cin / 32), 4 * BATCH, P * Cout, ctx);
     if (ks > 1) {
       int32_t* const part = static_cast<int32_t*>(ctx->work);
       hipLaunchKernelGGL(conv2d_i8_igemm<true>, dim3(pxb, chb, (unsigned)ks), dim3(256), 0, ctx->stream, X, W,

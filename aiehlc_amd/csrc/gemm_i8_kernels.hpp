@@ -239,21 +239,6 @@ __device__ __forceinline__ void pipe_epilogue(v16i (&acc)[NI][NJ], int8_t* lds, 
   }
 }
 
-// s_waitcnt vmcnt((n - 1) * CP) for a run-time 1 <= n <= N, with the count
-// as the immediate it must be: the copies of all but the first of n tiles
-// (CP per tile) may stay in flight.
-template <int CP, int N>
-__device__ __forceinline__ void wait_tiles_behind(int n) {
-  if constexpr (N > 1) {
-    if (n == N)
-      dev::wait_vmcnt<(N - 1) * CP>();
-    else
-      wait_tiles_behind<CP, N - 1>(n);
-  } else {
-    dev::wait_vmcnt<0>();
-  }
-}
-
 // The last S k-tiles of an S-stage pipeline, D = KT - kt of them left when
 // tile kt runs: tile kt+S-1 (whose second half this tile issues) exists for
 // D == S, tile kt+1 for D >= 2, and the D - 2 whole tiles after kt+1 stay in
@@ -405,7 +390,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
   if (KT >= S)
     dev::wait_vmcnt<(S - 2) * CP + CP_A>();
   else  // KT < S tiles, all issued whole: the KT - 1 after tile 0 may stay in flight
-    wait_tiles_behind<CP, S - 1>(KT);
+    dev::wait_tiles_behind<CP, S - 1>(KT);
   dev::barrier();
 
   Frags f0, f1;

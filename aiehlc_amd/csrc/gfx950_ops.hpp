@@ -43,6 +43,21 @@ __device__ __forceinline__ void waitcnt() {
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() { waitcnt<N, 15>(); }
 
+// s_waitcnt vmcnt((n - 1) * CP) for a run-time 1 <= n <= N, with the count
+// as the immediate it must be: the copies of all but the first of n tiles or
+// stages (CP per tile) may stay in flight.
+template <int CP, int N>
+__device__ __forceinline__ void wait_tiles_behind(int n) {
+  if constexpr (N > 1) {
+    if (n == N)
+      wait_vmcnt<(N - 1) * CP>();
+    else
+      wait_tiles_behind<CP, N - 1>(n);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
 // Workgroup barrier with no implied memory waits (callers wait explicitly).
 // The empty asm statements keep the compiler from moving memory accesses
 // across it.

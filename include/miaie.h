@@ -134,6 +134,7 @@ MIAIE_API int miaie_plan_set_cus(miaie_ctx* ctx, int cus, int* previous);
 #define MIAIE_CONV_ROWS 0   /* row-block kernel: 3x3, stride 1, Cin 32/64/128, Cout % 32 == 0, Wo <= 64 */
 #define MIAIE_CONV_IGEMM 1  /* implicit-GEMM kernel: Cin % 32 == 0, Cout % 64 == 0 */
 #define MIAIE_CONV_DIRECT 2 /* any shape, one thread per output element */
+#define MIAIE_CONV_TAPS 3   /* LDS-staged implicit GEMM over filter taps: Cin % 128 == 0, Cout % 64 == 0 */
 MIAIE_API int miaie_plan_conv2d_i8(int N, int H, int W, int Cin, int Cout, int R, int S, int stride, int pad,
                                    int* kernel);
 

@@ -65,6 +65,11 @@ def test_status_codes_match_header():
     for name in ("MIAIE_OK", "MIAIE_EINVAL", "MIAIE_EHIP", "MIAIE_ETIMEDOUT", "MIAIE_ENOMEM", "MIAIE_EUNSUPPORTED"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m and int(m.group(1)) == getattr(mi, name), name
+    # the conv planner's kernel ids, as the Python binding names them
+    for name, label in (("MIAIE_CONV_ROWS", "rows"), ("MIAIE_CONV_IGEMM", "igemm"), ("MIAIE_CONV_DIRECT", "direct"),
+                        ("MIAIE_CONV_TAPS", "taps")):
+        m = re.search(rf"#define {name} (\d+)", text)
+        assert m and mi.CONV_KERNELS[int(m.group(1))] == label, name
 
 
 def test_conv_planner_keeps_32_bit_offsets_in_range():
@@ -86,5 +91,11 @@ def test_conv_planner_keeps_32_bit_offsets_in_range():
     assert mi.plan_conv2d_i8(n_big, 56, 56, 64, 64) == "igemm"
     assert mi.plan_conv2d_i8(2, 56, 56, 64, 64, stride=2) == "igemm"
     assert mi.plan_conv2d_i8(1, 5, 5, 4, 8) == "direct"
+    # deep layers and wide rows with Cin a multiple of 128 take the LDS-staged taps kernel
+    assert mi.plan_conv2d_i8(8, 14, 14, 256, 256) == "taps"
+    assert mi.plan_conv2d_i8(8, 7, 7, 512, 512) == "taps"
+    assert mi.plan_conv2d_i8(8, 112, 112, 128, 128) == "taps"              # Wo > 64: not the row-block kernel
+    n_deep = (1 << 31) // (14 * 14 * 256) + 1                             # X reaches 2^31 bytes
+    assert mi.plan_conv2d_i8(n_deep, 14, 14, 256, 256) == "igemm"
     with pytest.raises(mi.MiaieError):
         mi.plan_conv2d_i8(1, 2, 2, 4, 4, 5, 5, 1, 0)                  # filter larger than the input

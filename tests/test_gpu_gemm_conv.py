@@ -259,11 +259,13 @@ CONV_SHAPES = [
     (2, 7, 28, 128, 128, 3, 3, 1, 1),  # row-block 2 x 64 at Cin 128 (108 KiB of LDS), odd Ho
     (1, 6, 60, 128, 96, 3, 3, 1, 2),  # row-block 4 x 32 at Cin 128, pad 2
     (1, 5, 9, 96, 64, 3, 3, 1, 1),    # Cin 96: implicit-GEMM kernel
-    (1, 8, 8, 256, 64, 3, 3, 1, 1),   # implicit GEMM, one tile split 3 ways over k (split-K partials + reduce)
-    (2, 7, 7, 512, 128, 3, 3, 1, 1),  # 4 tiles split 6 ways, the last pixel block partial
-    (1, 6, 6, 320, 64, 3, 3, 2, 1),   # stride 2, split over k
-    (8, 14, 14, 256, 256, 3, 3, 1, 1),  # deep CNN layer: 100 tiles, not split (fewer than 3 workgroups per tile fit)
-    (8, 7, 7, 512, 512, 3, 3, 1, 1),    # deepest: 56 tiles, split 4 ways
+    (1, 8, 8, 256, 64, 3, 3, 1, 1),   # taps kernel (LDS-staged), one tile split 3 ways over k (partials + reduce)
+    (2, 7, 7, 512, 128, 3, 3, 1, 1),  # taps: 4 tiles split 8 ways, the last pixel block partial
+    (1, 6, 6, 320, 64, 3, 3, 2, 1),   # Cin 320: implicit GEMM, stride 2, split over k
+    (1, 5, 70, 128, 64, 3, 3, 1, 1),  # taps: rows wider than 64 (left and right padding), not split
+    (1, 9, 9, 128, 128, 3, 3, 2, 1),  # taps, stride 2
+    (8, 14, 14, 256, 256, 3, 3, 1, 1),  # deep CNN layer on taps: 100 tiles, not split (fewer than 3 workgroups per tile fit)
+    (8, 7, 7, 512, 512, 3, 3, 1, 1),    # deepest, on taps: 56 tiles, split 4 ways
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # fallback kernel (channels not multiples of 32/64)
     (2, 6, 7, 3, 5, 3, 3, 2, 0),      # fallback kernel
 ]
@@ -292,7 +294,8 @@ def test_conv2d_i8(ctx, shape):
     (1, 5, 20, 32, 96, 3, 3, 1, 1),   # row-block 4 rows x 32 channels
     (1, 4, 24, 128, 64, 3, 3, 1, 1),  # row-block at Cin 128
     (1, 8, 8, 64, 64, 3, 3, 2, 1),    # implicit-GEMM kernel
-    (1, 8, 8, 256, 64, 3, 3, 1, 1),   # implicit GEMM split over k (requantize in the reduce kernel)
+    (1, 8, 8, 256, 64, 3, 3, 1, 1),   # taps kernel split over k (requantize in the reduce kernel)
+    (1, 5, 70, 128, 64, 3, 3, 1, 1),  # taps kernel, requantize in its own epilogue
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # direct kernel
 ])
 @pytest.mark.parametrize("small", [False, True])
