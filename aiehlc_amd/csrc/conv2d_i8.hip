@@ -187,19 +187,21 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
 // v_mfma_i32_32x32x32_i8 accumulator), so there is no cross-wave reduction;
 // with split K (grid.z) the tile's stages are divided among workgroups whose
 // int32 partials conv2d_i8_splitk_reduce adds.
-template <int CK>
+template <int TP, int TC>
 struct TapsGeom {
-  static_assert(CK == 128, "128 input channels per stage");
-  static constexpr int NS = 8;             // LDS stages in the ring
-  static constexpr int CPR = CK / 16;      // 16-byte chunks per staged row
-  static constexpr int OPB = 64 * CK;      // one operand (64 rows) of one stage
-  static constexpr int STAGE = 2 * OPB;    // X rows, then W rows
-  static constexpr int CPO = OPB / 4096;   // copies per thread per operand per stage (256 x 16 bytes each)
-  static constexpr int CPS = 2 * CPO;      // copies per thread per stage
-  static constexpr int KS = CK / 32;       // 32-wide k-steps per stage
-  static constexpr int YP = 48;            // epilogue: LDS pitch of one pixel's 32 output channels
-  static constexpr int LDS = NS * STAGE + 4 * 32 * YP;
-  static_assert(CPO >= 1 && LDS <= 163840, "taps kernel staging");
+  static constexpr int CK = 128;                    // input channels per stage
+  static constexpr int NS = TP * TC > 64 * 64 ? 4 : 8;  // LDS stages in the ring
+  static constexpr int CPR = CK / 16;               // 16-byte chunks per staged row
+  static constexpr int XB = TP * CK, WB = TC * CK;  // the two operands of one stage
+  static constexpr int STAGE = XB + WB;             // X rows, then W rows
+  static constexpr int CPX = XB / 4096, CPW = WB / 4096;  // copies per thread per stage (256 x 16 bytes each)
+  static constexpr int CPS = CPX + CPW;
+  static constexpr int KS = CK / 32;                // 32-wide k-steps per stage
+  static constexpr int NI = TP / 64, NJ = TC / 64;  // 32x32 blocks per wave (4 waves, 2 x 2)
+  static constexpr int YP = TC / 2 + 16;            // epilogue: LDS pitch of a pixel's TC/2 output channels
+  static constexpr int YW = TP / 2 * YP;            // one wave's output block
+  static constexpr int LDS = NS * STAGE + 4 * YW;
+  static_assert(CPX >= 1 && CPW >= 1 && NI >= 1 && NJ >= 1 && LDS <= 163840, "taps kernel staging");
   static_assert((NS - 2) * CPS <= 63, "copies in flight fit the vmcnt counter");
 };
 
@@ -207,51 +209,61 @@ struct TapsGeom {
 // fragment read touches land on distinct bank groups.
 __device__ __forceinline__ int taps_swz(int row) { return (row >> 1) & 7; }
 
-template <int CK, bool PARTIAL>
+// Workgroup tile TP output pixels x TC output channels (64 x 64 for small
+// grids, 128 x 128 otherwise); each wave owns TP/2 x TC/2, NI x NJ blocks of
+// 32 x 32.
+template <int TP, int TC, bool PARTIAL>
 __global__ __launch_bounds__(256) void conv2d_i8_taps(
     const int8_t* __restrict__ X, const int8_t* __restrict__ W, const uint8_t* __restrict__ shifts,
     int8_t* __restrict__ Y, int32_t* __restrict__ psum, int N, int H, int Wd, int Cin, int Cout, int R, int S,
     int stride, int pad, int Ho, int Wo, int ksplit) {
-  using G = TapsGeom<CK>;
+  using G = TapsGeom<TP, TC>;
+  constexpr int CK = G::CK, NI = G::NI, NJ = G::NJ;
   __shared__ __attribute__((aligned(1024))) int8_t lds[G::LDS];
   const uint32_t lds0 = miaie::dev::lds_addr(lds);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fh = lane >> 5;
-  const int pb = wave & 1, cb = wave >> 1;  // this wave's 32 pixels and 32 channels
+  const int pb = wave & 1, cb = wave >> 1;  // this wave's pixel half and channel half
   const int P = N * Ho * Wo;
-  const int p0 = blockIdx.x * 64, co0 = blockIdx.y * 64;
+  const int p0 = blockIdx.x * TP, co0 = blockIdx.y * TC;
   const int CB = Cin / CK, T = R * S * CB;
   const int sb = PARTIAL ? (int)((long long)T * blockIdx.z / ksplit) : 0;
   const int nst = (PARTIAL ? (int)((long long)T * (blockIdx.z + 1) / ksplit) : T) - sb;
   const int KW = R * S * Cin;
 
-  // ---- copy geometry.  Copy i (< CPO) of wave w moves 1 KiB block q = 4i + w
-  // of an operand: rows q * (1024 / CK) + lane / CPR, logical chunk
-  // (lane % CPR) ^ swz(row), landing at LDS byte q * 1024 + 16 * lane.
-  int xhb[G::CPO], xwb[G::CPO];
-  uint32_t xbase[G::CPO], wbase[G::CPO];
+  // ---- copy geometry.  Copy i of wave w moves 1 KiB block q = 4i + w of an
+  // operand: rows 8q + lane / 8, logical chunk (lane % 8) ^ swz(row), landing
+  // at LDS byte 1024 q + 16 lane of the operand.
+  int xhb[G::CPX], xwb[G::CPX];
+  uint32_t xbase[G::CPX], wbase[G::CPW];
   const uint32_t rowx = (uint32_t)Wd * Cin;  // bytes per input row
 #pragma unroll
-  for (int i = 0; i < G::CPO; ++i) {
-    const int row = (4 * i + wave) * (1024 / CK) + lane / G::CPR;
+  for (int i = 0; i < G::CPX; ++i) {
+    const int row = (4 * i + wave) * 8 + lane / G::CPR;
     const int gc = (lane % G::CPR) ^ taps_swz(row);
     const int p = min(p0 + row, P - 1);  // rows past the last pixel copy a real one (never stored)
     const int wo = p % Wo, t = p / Wo;
     xhb[i] = (t % Ho) * stride - pad;
     xwb[i] = wo * stride - pad;
     xbase[i] = (uint32_t)((t / Ho) * H) * rowx + (uint32_t)(16 * gc);
-    wbase[i] = (uint32_t)((co0 + row) * KW + 16 * gc);
   }
-  // this lane's fragment pixel (X rows 32pb + fr)
-  const int pf = p0 + 32 * pb + fr;
-  const bool pvalid = pf < P;
-  int fhb, fwb;
-  {
-    const int pp = pvalid ? pf : 0;
+#pragma unroll
+  for (int i = 0; i < G::CPW; ++i) {
+    const int row = (4 * i + wave) * 8 + lane / G::CPR;
+    wbase[i] = (uint32_t)((co0 + row) * KW + 16 * ((lane % G::CPR) ^ taps_swz(row)));
+  }
+  // this lane's fragment pixels (X rows TP/2 pb + 32 i + fr)
+  bool pvalid[NI];
+  int fhb[NI], fwb[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int pf = p0 + TP / 2 * pb + 32 * i + fr;
+    pvalid[i] = pf < P;
+    const int pp = pvalid[i] ? pf : 0;
     const int wo = pp % Wo, t = pp / Wo;
-    fhb = (t % Ho) * stride - pad;
-    fwb = wo * stride - pad;
+    fhb[i] = (t % Ho) * stride - pad;
+    fwb[i] = wo * stride - pad;
   }
 
   // A stage position (filter row r, column s, channel chunk c) walked
@@ -278,19 +290,27 @@ __global__ __launch_bounds__(256) void conv2d_i8_taps(
   auto issue = [&](const Tap& t, int slot) {
     const uint32_t base = lds0 + slot * G::STAGE + 1024 * wave;
     const uint32_t wk = (uint32_t)((t.r * S + t.s) * Cin + t.c * CK), xk = (uint32_t)(t.c * CK);
+    // X and W copies alternate (issuing all of one operand first measured 6%
+    // slower at 64 x 64)
 #pragma unroll
-    for (int i = 0; i < G::CPO; ++i) {
-      const int hi = min(max(xhb[i] + t.r, 0), H - 1), wi = min(max(xwb[i] + t.s, 0), Wd - 1);
-      const uint32_t xoff = xbase[i] + (uint32_t)hi * rowx + (uint32_t)wi * Cin + xk;
-      miaie::dev::gload_lds16(X, xoff, base + 4096 * i);
-      miaie::dev::gload_lds16(W, wbase[i] + wk, base + G::OPB + 4096 * i);
+    for (int i = 0; i < (G::CPX > G::CPW ? G::CPX : G::CPW); ++i) {
+      if (i < G::CPX) {
+        const int hi = min(max(xhb[i] + t.r, 0), H - 1), wi = min(max(xwb[i] + t.s, 0), Wd - 1);
+        miaie::dev::gload_lds16(X, xbase[i] + (uint32_t)hi * rowx + (uint32_t)wi * Cin + xk, base + 4096 * i);
+      }
+      if (i < G::CPW) miaie::dev::gload_lds16(W, wbase[i] + wk, base + G::XB + 4096 * i);
     }
   };
 
-  v16i acc = v16i{0};
-  const int8_t* const wfrag = lds + G::OPB + (32 * cb + fr) * CK;
-  const int8_t* const xfrag = lds + (32 * pb + fr) * CK;
-  const int wsw = taps_swz(32 * cb + fr), xsw = taps_swz(32 * pb + fr);
+  v16i acc[NJ][NI];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int i = 0; i < NI; ++i) acc[j][i] = v16i{0};
+  const int8_t* const wfrag = lds + G::XB + (TC / 2 * cb + fr) * CK;
+  const int8_t* const xfrag = lds + (TP / 2 * pb + fr) * CK;
+  // the swizzle of rows r and r + 32 is the same: one per operand
+  const int wsw = taps_swz(TC / 2 * cb + fr), xsw = taps_swz(TP / 2 * pb + fr);
 
 #pragma unroll
   for (int i = 0; i < G::NS - 1; ++i)
@@ -308,46 +328,77 @@ __global__ __launch_bounds__(256) void conv2d_i8_taps(
       issue(at_issue, (s + G::NS - 1) % G::NS);
       step(at_issue);
     }
-    const bool xin = pvalid && (unsigned)(fhb + at_use.r) < (unsigned)H && (unsigned)(fwb + at_use.s) < (unsigned)Wd;
+    bool xin[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      xin[i] = pvalid[i] && (unsigned)(fhb[i] + at_use.r) < (unsigned)H && (unsigned)(fwb[i] + at_use.s) < (unsigned)Wd;
     step(at_use);
     const int slot = (s % G::NS) * G::STAGE;
 #pragma unroll
     for (int ks = 0; ks < G::KS; ++ks) {
-      const v4i wf = *reinterpret_cast<const v4i*>(wfrag + slot + (((2 * ks + fh) ^ wsw) << 4));
-      v4i xf = *reinterpret_cast<const v4i*>(xfrag + slot + (((2 * ks + fh) ^ xsw) << 4));
-      xf = xin ? xf : v4i{0};
-      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, xf, acc, 0, 0, 0);
+      const int cw = ((2 * ks + fh) ^ wsw) << 4, cx = ((2 * ks + fh) ^ xsw) << 4;
+      v4i wf[NJ], xf[NI];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) wf[j] = *reinterpret_cast<const v4i*>(wfrag + slot + 32 * CK * j + cw);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        xf[i] = *reinterpret_cast<const v4i*>(xfrag + slot + 32 * CK * i + cx);
+        xf[i] = xin[i] ? xf[i] : v4i{0};
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[j], xf[i], acc[j][i], 0, 0, 0);
     }
   }
 
-  // acc[4g + t]: channel 32cb + 8g + 4fh + t, pixel pf
-  const int cq = co0 + 32 * cb + 4 * fh;
+  // acc[j][i][4g + t]: channel TC/2 cb + 32j + 8g + 4fh + t, pixel TP/2 pb + 32i + fr
   if constexpr (PARTIAL) {
-    if (pvalid) {
-      int32_t* const dst = psum + ((size_t)blockIdx.z * P + pf) * Cout + cq;
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<v4i*>(dst + 8 * g) = v4i{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+    for (int i = 0; i < NI; ++i) {
+      const int pf = p0 + TP / 2 * pb + 32 * i + fr;
+      if (!pvalid[i]) continue;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        int32_t* const dst = psum + ((size_t)blockIdx.z * P + pf) * Cout + co0 + TC / 2 * cb + 32 * j + 4 * fh;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<v4i*>(dst + 8 * g) =
+              v4i{acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]};
+      }
     }
     return;
   }
-  // requantize into this wave's own LDS block, then 16-byte stores, two
-  // lanes per pixel's 32 channels (an LDS wait, no workgroup barrier)
-  int8_t* const yb = lds + G::NS * G::STAGE + wave * 32 * G::YP;
+  // requantize into this wave's own LDS block (TP/2 pixels x TC/2 channels),
+  // then 16-byte stores of whole pixel runs (an LDS wait, no workgroup barrier)
+  int8_t* const yb = lds + G::NS * G::STAGE + wave * G::YW;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const uint32_t sh = *reinterpret_cast<const uint32_t*>(shifts + cq + 8 * g);
-    uint32_t v = 0;
+  for (int j = 0; j < NJ; ++j) {
+    const int cl = 32 * j + 4 * fh;  // channel within the wave's half
 #pragma unroll
-    for (int t = 0; t < 4; ++t) v |= (uint32_t)(requant1(acc[4 * g + t], (sh >> (8 * t)) & 0xFF) & 0xFF) << (8 * t);
-    *reinterpret_cast<uint32_t*>(yb + fr * G::YP + 8 * g + 4 * fh) = v;
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t sh = *reinterpret_cast<const uint32_t*>(shifts + co0 + TC / 2 * cb + cl + 8 * g);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          v |= (uint32_t)(requant1(acc[j][i][4 * g + t], (sh >> (8 * t)) & 0xFF) & 0xFF) << (8 * t);
+        *reinterpret_cast<uint32_t*>(yb + (32 * i + fr) * G::YP + cl + 8 * g) = v;
+      }
+    }
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
   __builtin_amdgcn_wave_barrier();
-  const int sp = lane >> 1, sh = lane & 1;
-  if (p0 + 32 * pb + sp < P) {
-    const v4i v = *reinterpret_cast<const v4i*>(yb + sp * G::YP + 16 * sh);
-    *reinterpret_cast<v4i*>(Y + (size_t)(p0 + 32 * pb + sp) * Cout + co0 + 32 * cb + 16 * sh) = v;
+  constexpr int CPP = TC / 32;  // 16-byte chunks per pixel of the wave's half
+#pragma unroll
+  for (int it = 0; it < TP / 2 * CPP / 64; ++it) {
+    const int flat = 64 * it + lane, sp = flat / CPP, ch = flat % CPP;
+    const int p = p0 + TP / 2 * pb + sp;
+    if (p < P) {
+      const v4i v = *reinterpret_cast<const v4i*>(yb + sp * G::YP + 16 * ch);
+      *reinterpret_cast<v4i*>(Y + (size_t)p * Cout + co0 + TC / 2 * cb + 16 * ch) = v;
+    }
   }
 }
 
@@ -476,22 +527,30 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
     return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
   }
   if (kernel == MIAIE_CONV_TAPS) {
-    const unsigned pxb = (unsigned)((P + 63) / 64), chb = (unsigned)(Cout / 64);
-    const int ks = conv_ksplit((size_t)pxb * chb, R * S * (Cin / 128), 4, P * Cout, ctx);
+    // 128 x 128 tiles when they fill at least one round of CUs, else 64 x 64
+    // (split over k when even those leave most CUs idle)
+    const bool big = Cout % 128 == 0 && ((P + 127) / 128) * (size_t)(Cout / 128) >= (size_t)ctx->cus;
+    const int tp = big ? 128 : 64;
+    const unsigned pxb = (unsigned)((P + tp - 1) / tp), chb = (unsigned)(Cout / tp);
+    const int ks = big ? 1 : conv_ksplit((size_t)pxb * chb, R * S * (Cin / 128), 4, P * Cout, ctx);
     auto go = [&](auto kernel, unsigned z, int32_t* psum) {
       hipLaunchKernelGGL(kernel, dim3(pxb, chb, z), dim3(256), 0, ctx->stream, X, W, shifts, Y, psum, N, H, Wd, Cin,
                          Cout, R, S, stride, pad, Ho, Wo, (int)z);
     };
+    if (big) {
+      go(conv2d_i8_taps<128, 128, false>, 1u, nullptr);
+      return check_launch(ctx, "conv2d_i8_taps (128 x 128)");
+    }
     if (ks > 1) {
       int32_t* const psum = static_cast<int32_t*>(ctx->work);
-      go(conv2d_i8_taps<128, true>, (unsigned)ks, psum);
+      go(conv2d_i8_taps<64, 64, true>, (unsigned)ks, psum);
       if (int rc = check_launch(ctx, "conv2d_i8_taps (split K)")) return rc;
       const long long PC = (long long)(P * Cout);
       hipLaunchKernelGGL(conv2d_i8_splitk_reduce, dim3((unsigned)((PC / 16 + 255) / 256)), dim3(256), 0,
                          ctx->stream, psum, shifts, Y, PC, Cout, ks);
       return check_launch(ctx, "conv2d_i8_splitk_reduce");
     }
-    go(conv2d_i8_taps<128, false>, 1u, nullptr);
+    go(conv2d_i8_taps<64, 64, false>, 1u, nullptr);
     return check_launch(ctx, "conv2d_i8_taps");
   }
   if (kernel == MIAIE_CONV_IGEMM) {

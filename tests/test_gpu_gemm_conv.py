@@ -290,6 +290,37 @@ def test_conv2d_i8(ctx, shape):
 
 
 @pytest.mark.parametrize("shape", [
+    (1, 9, 70, 128, 128, 3, 3, 1, 1),   # 5 pixel tiles, the last partial
+    (2, 7, 7, 256, 256, 3, 3, 1, 1),    # one partial pixel tile, two channel tiles
+    (1, 17, 17, 128, 256, 3, 3, 2, 1),  # stride 2
+    (1, 6, 6, 384, 128, 3, 3, 1, 0),    # no padding, three 128-channel chunks per tap
+])
+def test_conv2d_i8_taps_128_tiles(ctx, shape):
+    """The taps kernel's 128 x 128 workgroup tile, which the launcher takes
+    when those tiles fill a round of CUs: planned here for one CU so that
+    small shapes take it.  Bit-exact against the oracle."""
+    N, H, W, Cin, Cout, R, S, stride, pad = shape
+    _say("conv2d taps 128x128", shape)
+    assert mi.plan_conv2d_i8(N, H, W, Cin, Cout, R, S, stride, pad) == "taps"
+    rng = np.random.default_rng(sum(shape) + 7)
+    X = rng.integers(-128, 128, size=(N, H, W, Cin), dtype=np.int8)
+    Wt = rng.integers(-128, 128, size=(Cout, R, S, Cin), dtype=np.int8)
+    sh = rng.integers(8, 13, size=Cout, dtype=np.uint8)
+    Ho = (H + 2 * pad - R) // stride + 1
+    Wo = (W + 2 * pad - S) // stride + 1
+    prev = ctx.plan_set_cus(1)
+    try:
+        dX, dW, dS = ctx.upload(X), ctx.upload(Wt), ctx.upload(sh)
+        dY = ctx.empty((N, Ho, Wo, Cout), np.int8)
+        ctx.conv2d_i8_nhwc(dX, dW, dS, dY, N, H, W, Cin, Cout, R, S, stride, pad)
+        ctx.wait(60_000)
+        Yg = ctx.download(dY)
+    finally:
+        ctx.plan_set_cus(prev)
+    assert np.array_equal(Yg, oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad))
+
+
+@pytest.mark.parametrize("shape", [
     (1, 6, 56, 64, 64, 3, 3, 1, 1),   # row-block 2 rows x 64 channels
     (1, 5, 20, 32, 96, 3, 3, 1, 1),   # row-block 4 rows x 32 channels
     (1, 4, 24, 128, 64, 3, 3, 1, 1),  # row-block at Cin 128
