@@ -475,6 +475,35 @@ def extra_ragged(ctx, timer, args) -> dict:
     return out
 
 
+def extra_conv_shapes(ctx, timer, args) -> dict:
+    """int8 conv2d 3x3 (stride 1, pad 1, per-channel shifts) on CNN layer
+    shapes beyond config 4, with the kernel the planner picks for each: wide
+    rows, deep layers (few pixels, long k) and large layers.  Back-to-back
+    calls through the Python binding (its ctypes call adds about 0.5 us per
+    call on small shapes)."""
+    import aiehlc_amd as mi
+
+    out = {}
+    for N, H, Ci, Co in ((8, 112, 64, 64), (8, 112, 128, 128), (8, 56, 256, 256), (8, 14, 256, 256),
+                         (8, 7, 512, 512)):
+        dX, dW, dS, dY = (ctx.empty((N, H, H, Ci), np.int8), ctx.empty((Co, 3, 3, Ci), np.int8),
+                          ctx.empty((Co,), np.uint8), ctx.empty((N, H, H, Co), np.int8))
+        ctx.fill_i8(dX, N * H * H * Ci, 3)
+        ctx.fill_i8(dW, Co * 9 * Ci, 4)
+        ctx.copy_h2d(dS, mi.synth.shifts(Co, 7))
+        fn = lambda: ctx.conv2d_i8_nhwc(dX, dW, dS, dY, N, H, H, Ci, Co, 3, 3, 1, 1)
+        settle(ctx, fn, min(args.settle, 0.1))
+        ms = timed(ctx, timer, fn, 100, 10)
+        ops = 2.0 * N * H * H * Co * Ci * 9
+        byts = N * H * H * (Ci + Co) + Co * 9 * Ci + Co
+        out[f"{N}x{H}x{H}x{Ci}->{Co}"] = {"kernel": mi.plan_conv2d_i8(N, H, H, Ci, Co), "us": round(ms * 1e3, 2),
+                                          "tops": round(ops / (ms * 1e-3) / 1e12, 1),
+                                          "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 3)}
+        for b in (dX, dW, dS, dY):
+            b.free()
+    return out
+
+
 def extra_bf16(ctx, timer, args) -> dict:
     """Config 3: bf16 8192^3, fp32 accumulate and output."""
     import aiehlc_amd as mi
@@ -522,7 +551,8 @@ def extra_mlp(ctx, timer, args) -> dict:
             "frac_of_peak": round(mops / (ms_m * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
 
 
-EXTRAS = {"conv": extra_conv, "m_shard": extra_m_shard, "bf16": extra_bf16, "mlp": extra_mlp, "ragged": extra_ragged}
+EXTRAS = {"conv": extra_conv, "m_shard": extra_m_shard, "bf16": extra_bf16, "mlp": extra_mlp, "ragged": extra_ragged,
+          "conv_shapes": extra_conv_shapes}
 
 
 def main() -> int:
@@ -588,6 +618,7 @@ def main() -> int:
         extras["gemm_bf16_8192"] = extra_bf16(ctx, timer, args)
         extras["mlp_i8"] = extra_mlp(ctx, timer, args)
         extras["gemm_ragged"] = extra_ragged(ctx, timer, args)
+        extras["conv2d_other_shapes"] = extra_conv_shapes(ctx, timer, args)
     ctx.close()
     if not args.no_extras:
         extras["mfma_ceiling"] = mfma_ceiling()
