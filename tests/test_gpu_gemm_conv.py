@@ -289,6 +289,41 @@ def test_conv2d_i8(ctx, shape):
     assert np.array_equal(Yg, oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad))
 
 
+def _random_conv_cases(n=16, seed=1202):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        Cin = int(rng.choice([3, 32, 64, 96, 128, 256, 384]))
+        Cout = int(rng.choice([8, 32, 64, 96, 128, 192, 256]))
+        R = int(rng.choice([1, 3, 3, 3, 5]))
+        stride = int(rng.choice([1, 1, 2]))
+        pad = int(rng.integers(0, R // 2 + 1))
+        H = int(rng.integers(R, 20))
+        W = int(rng.integers(R, 80))
+        N = int(rng.integers(1, 4))
+        cases.append((N, H, W, Cin, Cout, R, R, stride, pad))
+    return cases
+
+
+@pytest.mark.parametrize("shape", _random_conv_cases())
+def test_conv2d_i8_random_shapes(ctx, shape):
+    """Seeded random shapes over all four conv kernels (whichever the planner
+    picks), shifts over [0, 31], bit-exact against the oracle."""
+    N, H, W, Cin, Cout, R, S, stride, pad = shape
+    _say("conv2d random", shape, mi.plan_conv2d_i8(N, H, W, Cin, Cout, R, S, stride, pad))
+    rng = np.random.default_rng(sum(shape) * 13)
+    X = rng.integers(-128, 128, size=(N, H, W, Cin), dtype=np.int8)
+    Wt = rng.integers(-128, 128, size=(Cout, R, S, Cin), dtype=np.int8)
+    sh = rng.integers(0, 32, size=Cout, dtype=np.uint8)
+    Ho = (H + 2 * pad - R) // stride + 1
+    Wo = (W + 2 * pad - S) // stride + 1
+    dX, dW, dS = ctx.upload(X), ctx.upload(Wt), ctx.upload(sh)
+    dY = ctx.empty((N, Ho, Wo, Cout), np.int8)
+    ctx.conv2d_i8_nhwc(dX, dW, dS, dY, N, H, W, Cin, Cout, R, S, stride, pad)
+    ctx.wait(60_000)
+    assert np.array_equal(ctx.download(dY), oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad))
+
+
 @pytest.mark.parametrize("shape", [
     (1, 9, 70, 128, 128, 3, 3, 1, 1),   # 5 pixel tiles, the last partial
     (2, 7, 7, 256, 256, 3, 3, 1, 1),    # one partial pixel tile, two channel tiles

@@ -322,3 +322,51 @@ def test_mixed_tiles_match_the_oracle(ctx, M, N, K, cus, layout):
     assert np.array_equal(C2, Co)
     assert np.array_equal(Y, oracle.requant(Co, 10))
     assert np.array_equal(Y2, oracle.requant(Co, 5, relu=True))
+
+
+# Seeded random shapes across every planner branch (uniform, mixed and ragged
+# pipelined tiles, the 64x64 fallbacks), both B layouts, every output mode and
+# shifts on both sides of 8, each against the oracle.  Sizes are drawn so that
+# the pipelined kernels' conditions (K % 64, N % 16, M and N at least one
+# tile) are met about half the time.
+def _random_gemm_cases(n=24, seed=20261202):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        M = int(rng.choice([int(rng.integers(1, 130)), int(rng.integers(128, 1100))]))
+        N = int(rng.choice([int(rng.integers(1, 130)), 16 * int(rng.integers(8, 70)), int(rng.integers(128, 1100))]))
+        K = int(rng.choice([64 * int(rng.integers(1, 9)), 16 * int(rng.integers(1, 40)), int(rng.integers(1, 300))]))
+        cases.append((M, N, K, int(rng.integers(0, 2)), int(rng.integers(3, 14)), bool(rng.integers(0, 2)),
+                      int(rng.choice([0, 1, 4, 256]))))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,layout,shift,relu,cus", _random_gemm_cases())
+def test_random_shapes_match_the_oracle(ctx, M, N, K, layout, shift, relu, cus):
+    prev = ctx.plan_set_cus(cus) if cus else None
+    try:
+        plan = ctx.plan_gemm_i8(M, N, K)
+        print(f"[case] random gemm {M}x{N}x{K} layout {layout} shift {shift} relu {relu} cus {cus} plan {plan}",
+              flush=True)
+        rng = np.random.default_rng(M * 1009 + N * 31 + K)
+        A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+        B = rng.integers(-128, 128, size=(N, K) if layout == mi.B_NT else (K, N), dtype=np.int8)
+        dA, dB = ctx.upload(A), ctx.upload(B)
+        dC, dY, dY2, dC2 = (ctx.empty((M, N), np.int32), ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int8),
+                            ctx.empty((M, N), np.int32))
+        ctx.gemm_i8_i32(dA, dB, dC, M, N, K, b_layout=layout)
+        ctx.gemm_i8_rq(dA, dB, dY, M, N, K, shift, relu, None, layout)
+        ctx.gemm_i8_rq(dA, dB, dY2, M, N, K, shift, relu, dC2, layout)
+        ctx.wait(60_000)
+        C, Y, Y2, C2 = (ctx.download(d) for d in (dC, dY, dY2, dC2))
+        for b in (dA, dB, dC, dY, dY2, dC2):
+            b.free()
+    finally:
+        if cus:
+            ctx.plan_set_cus(prev)
+    Co = oracle.gemm_i8(A, B, b_nt=layout == mi.B_NT)
+    Yo = oracle.requant(Co, shift, relu=relu)
+    assert np.array_equal(C, Co)
+    assert np.array_equal(C2, Co)
+    assert np.array_equal(Y, Yo)
+    assert np.array_equal(Y2, Yo)
