@@ -180,6 +180,41 @@ def test_gemm_bf16_ragged_256(ctx, shape, cus):
     assert err <= 1e-5, err
 
 
+def _random_bf16_cases(n=12, seed=7):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        M = int(rng.choice([int(rng.integers(1, 300)), int(rng.integers(256, 900))]))
+        N = int(rng.choice([int(rng.integers(1, 300)), 8 * int(rng.integers(32, 110))]))
+        K = int(rng.choice([32 * int(rng.integers(1, 20)), int(rng.integers(1, 400))]))
+        cases.append((M, N, K, int(rng.choice([0, 1]))))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,one_cu", _random_bf16_cases())
+def test_gemm_bf16_random_shapes(ctx, M, N, K, one_cu):
+    """Seeded random shapes; planned for one CU half the time, so that
+    ragged shapes take the 256x256 kernels with overlapping last tiles."""
+    _say("gemm_bf16 random", (M, N, K), "one CU" if one_cu else "")
+    A = synth.bf16_normal((M, K), 8, 1.0 / np.sqrt(K))
+    B = synth.bf16_normal((K, N), 9, 1.0 / np.sqrt(K))
+    prev = ctx.plan_set_cus(1) if one_cu else None
+    try:
+        dA, dB, dC = ctx.upload(A), ctx.upload(B), ctx.empty((M, N), np.float32)
+        ctx.gemm_bf16_f32(dA, dB, dC, M, N, K)
+        ctx.wait(60_000)
+        Cg = ctx.download(dC).astype(np.float64)
+        for b in (dA, dB, dC):
+            b.free()
+    finally:
+        if one_cu:
+            ctx.plan_set_cus(prev)
+    R = oracle.gemm_bf16(A, B, f64=True)
+    err = np.abs(Cg - R).max() / max(np.abs(R).max(), 1e-30)
+    assert err <= BF16_TOL, err
+    assert err <= 1e-5, err
+
+
 # K sweep over the 256x256 bf16 kernels: K % 64 == 0 takes the pair-staged
 # kernel (A staged two k-tiles at a time; its waits change over the last six
 # k-tiles and in the prologue below six), odd multiples of 32 the per-k-tile
