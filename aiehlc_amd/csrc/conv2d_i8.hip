@@ -480,11 +480,12 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
   const int Ho = (H + 2 * pad - R) / stride + 1;
   const int Wo = (Wd + 2 * pad - S) / stride + 1;
   const size_t P = (size_t)N * Ho * Wo;
-  // Row-block kernel (3x3, stride 1, Cin 32, 64 or 128, Wo <= 64).  Its
-  // offsets are 32-bit: X, Y and W (co0 * R*S*Cin) must each stay below
-  // 2^31 bytes, and the channel blocks (>= 32 channels each) fit grid.y.
+  // Row-block kernel (3x3, stride 1, Cin 32, 64 or 128; rows wider than 64
+  // output columns in blocks of 64).  Its offsets are 32-bit: X, Y and W
+  // (co0 * R*S*Cin) must each stay below 2^31 bytes, and the channel blocks
+  // (>= 32 channels each) fit grid.y.
   const bool rows_ok = stride == 1 && R == 3 && S == 3 && (Cin == 32 || Cin == 64 || Cin == 128) && Cout % 32 == 0 &&
-                       Wo <= conv::PB && aligned16 && shifts_aligned4 && N <= 65535 &&
+                       aligned16 && shifts_aligned4 && N <= 65535 &&
                        (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31) &&
                        (size_t)Cout * R * S * Cin < ((size_t)1 << 31) && Cout / 32 <= 65535;
   if (rows_ok) return MIAIE_CONV_ROWS;

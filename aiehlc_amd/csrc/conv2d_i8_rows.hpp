@@ -1,10 +1,11 @@
 // Row-block int8 conv2d kernel (device code), shared by the library
 // (conv2d_i8.hip) and the in-kernel clock probe (probes/conv_span.hip).
 //
-// For stride-1 convolutions with Wo <= 64 (instantiated for 3x3 filters and
-// Cin in {32, 64, 128}).  A workgroup owns ROWS output rows of one image (64
-// columns, padded) and one block of WCO output channels, with ROWS * WCO =
-// 128 so that its 8 waves each own 32 pixels x 32 channels.  It stages in LDS
+// For stride-1 convolutions (instantiated for 3x3 filters and Cin in {32,
+// 64, 128}).  A workgroup owns ROWS output rows of one image, 64 columns of
+// them (padded; wider rows are cut into blocks of 64 columns), and one block
+// of WCO output channels, with ROWS * WCO = 128 so that its 8 waves each own
+// 32 pixels x 32 channels.  It stages in LDS
 // once, with every global load of the staging in flight together:
 //   X  the ROWS+R-1 input rows the output rows touch, with the zero padding
 //      columns and rows materialised, [row][col][Cin bytes], 16-byte chunk
@@ -77,12 +78,14 @@ struct RowsGeom {
 constexpr int PROBE_WORDS = 6;
 
 // xg: 0 for the (row blocks, channel blocks, N) grid, else N / 8 for the
-// image-per-XCD grid.  probe: PROBE_WORDS words per wave (TIMED only).
+// image-per-XCD grid.  ncb: blocks of PB output columns per row (rows wider
+// than PB are split; the row-block grid index counts row block x ncb +
+// column block).  probe: PROBE_WORDS words per wave (TIMED only).
 template <int R, int S, int CIN, int ROWS, int WCO, bool TIMED>
 __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
                                                       const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
                                                       int H, int Wd, int Cout, int pad, int Ho, int Wo, int xg,
-                                                      unsigned long long* __restrict__ probe) {
+                                                      int ncb, unsigned long long* __restrict__ probe) {
   using G = RowsGeom<R, S, CIN, ROWS, WCO>;
   __shared__ __attribute__((aligned(16))) int8_t smem[G::LDS];
   unsigned long long t0 = 0, r0 = 0;
@@ -102,6 +105,12 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
     rb = blockIdx.x;
     cb = blockIdx.y;
     n = blockIdx.z;
+  }
+  int wc0 = 0;  // first output column of this block
+  if (ncb > 1) {
+    const int cbk = rb % ncb;
+    rb /= ncb;
+    wc0 = cbk * PB;
   }
   const int ho0 = rb * ROWS;
   const int co0 = cb * WCO;
@@ -130,7 +139,7 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   const int et = tid % G::XE;
   const int ec = et % G::NCH, ecol = PB + (et / G::NCH) % (G::XC - PB), erow = et / (G::NCH * (G::XC - PB));
   auto x_off = [&](int row, int col, int c, bool& in) -> uint32_t {
-    const int hi = ho0 + row - pad, wi = col - pad;
+    const int hi = ho0 + row - pad, wi = wc0 + col - pad;
     in = (unsigned)hi < (unsigned)H && (unsigned)wi < (unsigned)Wd;
     // clamped into the image: a valid address without a branch
     const int hc = min(max(hi, 0), H - 1), wcl = min(max(wi, 0), Wd - 1);
@@ -236,9 +245,10 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
     __builtin_amdgcn_wave_barrier();
     const int sp = 32 * pb + (lane >> 1), sh = lane & 1;
-    if (sp < Wo && ho0 + rr < Ho) {
+    if (wc0 + sp < Wo && ho0 + rr < Ho) {
       const v4i v = *reinterpret_cast<const v4i*>(ys + (rr * PB + sp) * G::YP + 32 * wc + 16 * sh);
-      *reinterpret_cast<v4i*>(Y + (uint32_t)(((n * Ho + ho0 + rr) * Wo + sp) * Cout + co0 + 32 * wc + 16 * sh)) = v;
+      *reinterpret_cast<v4i*>(Y + (uint32_t)(((n * Ho + ho0 + rr) * Wo + wc0 + sp) * Cout + co0 + 32 * wc + 16 * sh)) =
+          v;
     }
   }
   if constexpr (TIMED) {
@@ -257,11 +267,12 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
 template <int CIN, int ROWS, int WCO, bool TIMED>
 inline void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
                            int H, int Wd, int Cout, int pad, int Ho, int Wo, unsigned long long* probe = nullptr) {
-  const unsigned rbs = (unsigned)((Ho + ROWS - 1) / ROWS), cbs = (unsigned)(Cout / WCO);
+  const int ncb = (Wo + PB - 1) / PB;
+  const unsigned rbs = (unsigned)((Ho + ROWS - 1) / ROWS * ncb), cbs = (unsigned)(Cout / WCO);
   const bool by_xcd = N % 8 == 0 && rbs <= 65535 && (size_t)(N / 8) * cbs <= 65535;
   const dim3 grid = by_xcd ? dim3(8, rbs, (unsigned)(N / 8) * cbs) : dim3(rbs, cbs, (unsigned)N);
   hipLaunchKernelGGL((conv2d_i8_rows<3, 3, CIN, ROWS, WCO, TIMED>), grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd,
-                     Cout, pad, Ho, Wo, by_xcd ? N / 8 : 0, probe);
+                     Cout, pad, Ho, Wo, by_xcd ? N / 8 : 0, ncb, probe);
 }
 
 }  // namespace conv

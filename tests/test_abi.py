@@ -91,10 +91,11 @@ def test_conv_planner_keeps_32_bit_offsets_in_range():
     assert mi.plan_conv2d_i8(n_big, 56, 56, 64, 64) == "igemm"
     assert mi.plan_conv2d_i8(2, 56, 56, 64, 64, stride=2) == "igemm"
     assert mi.plan_conv2d_i8(1, 5, 5, 4, 8) == "direct"
-    # deep layers and wide rows with Cin a multiple of 128 take the LDS-staged taps kernel
+    # deep layers (Cin a multiple of 128 above 128) and strided ones take the LDS-staged taps kernel
     assert mi.plan_conv2d_i8(8, 14, 14, 256, 256) == "taps"
     assert mi.plan_conv2d_i8(8, 7, 7, 512, 512) == "taps"
-    assert mi.plan_conv2d_i8(8, 112, 112, 128, 128) == "taps"              # Wo > 64: not the row-block kernel
+    assert mi.plan_conv2d_i8(8, 112, 112, 128, 128) == "rows"              # rows wider than 64: column blocks
+    assert mi.plan_conv2d_i8(8, 112, 112, 128, 128, stride=2) == "taps"     # stride 2: not the row-block kernel
     n_deep = (1 << 31) // (14 * 14 * 256) + 1                             # X reaches 2^31 bytes
     assert mi.plan_conv2d_i8(n_deep, 14, 14, 256, 256) == "igemm"
     with pytest.raises(mi.MiaieError):

@@ -360,7 +360,7 @@ def test_conv2d_i8_random_shapes(ctx, shape):
 
 
 @pytest.mark.parametrize("shape", [
-    (1, 9, 70, 128, 128, 3, 3, 1, 1),   # 5 pixel tiles, the last partial
+    (1, 9, 70, 256, 128, 3, 3, 1, 1),   # 5 pixel tiles, the last partial
     (2, 7, 7, 256, 256, 3, 3, 1, 1),    # one partial pixel tile, two channel tiles
     (1, 17, 17, 128, 256, 3, 3, 2, 1),  # stride 2
     (1, 6, 6, 384, 128, 3, 3, 1, 0),    # no padding, three 128-channel chunks per tap
