@@ -115,7 +115,7 @@ def header_functions(path: str = HEADER_PATH) -> list[str]:
     return re.findall(r"MIAIE_API\s+[\w\s\*]+?\b(miaie_\w+)\s*\(", text)
 
 
-CONV_KERNELS = {0: "rows", 1: "igemm", 2: "direct", 3: "taps"}  # MIAIE_CONV_*
+CONV_KERNELS = {0: "rows", 1: "igemm", 2: "direct", 3: "taps", 4: "rows_deep"}  # MIAIE_CONV_*
 
 
 def plan_conv2d_i8(N, H, W, Cin, Cout, R=3, S=3, stride=1, pad=1) -> str:

@@ -475,6 +475,59 @@ static int launch_rows(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const u
   return check_launch(ctx, "conv2d_i8_rows");
 }
 
+// Workgroups per tile of the implicit-GEMM kernels (1: no split).  Split
+// when at least 3 workgroups per tile fit on the CUs (a 2-way split measured
+// no faster: the reduce kernel's launch costs what the halved k-chain
+// saves), into at most 8 and at most cus / tiles parts, each keeping at least
+// min_per_split k-steps, with the partial sums inside the context's
+// workspace of work_bytes.
+static int conv_ksplit(size_t tiles, int T, int min_per_split, size_t elems, int cus, size_t work_bytes) {
+  if (tiles * 3 > (size_t)cus) return 1;
+  int ks = (int)std::min<size_t>((size_t)cus / tiles, 8);
+  ks = std::min(ks, T / min_per_split);
+  while (ks > 1 && (size_t)ks * elems * sizeof(int32_t) > work_bytes) --ks;
+  return ks > 1 ? ks : 1;
+}
+
+// Estimated time of a launch (microseconds), for choosing between the
+// chunked row-block kernel and the taps kernel: rounds of one workgroup per
+// CU times a per-workgroup time fitted to back-to-back launches on MI355X
+// (8x{56,28,14,7}^2 layers, Cin and Cout 256 and 512, 1x224^2x256 and
+// 32x{28,14}^2 layers): a fixed start and end cost plus a cost per 64-channel
+// chunk or per taps stage.
+static double launch_rounds(size_t wgs, int cus) { return (double)((wgs + cus - 1) / cus); }
+
+// conv2d_i8_rowsk<4, 32*nj, nj>: 8 waves of 32 pixels x 32*nj channels
+static double rows_deep_us(int N, int Ho, int Wo, int Cin, int Cout, int nj, int cus) {
+  const size_t wgs = (size_t)N * ((Ho + 3) / 4) * ((Wo + conv::PB - 1) / conv::PB) * (size_t)(Cout / (32 * nj));
+  const int nk = Cin / 64;
+  return launch_rounds(wgs, cus) * (nj == 2 ? 3.5 + 1.68 * nk : 2.8 + 1.0 * nk);
+}
+
+// Wave tile of the chunked row-block kernel: 32 x 64 (two MFMAs per pixel
+// fragment, 3/4 of the LDS reads per MAC) unless it leaves so few workgroups
+// that 32 x 32 finishes first.
+static int rows_deep_nj(int N, int Ho, int Wo, int Cin, int Cout, int cus) {
+  if (Cout % 64) return 1;
+  return rows_deep_us(N, Ho, Wo, Cin, Cout, 2, cus) <= rows_deep_us(N, Ho, Wo, Cin, Cout, 1, cus) ? 2 : 1;
+}
+
+// conv2d_i8_taps as its launcher runs it: 128 x 128 tiles when they fill a
+// round of CUs, else 64 x 64 split over k; a stage is one tap x 128 channels.
+static double taps_us(size_t P, int Cin, int Cout, int R, int S, int cus, size_t work_bytes) {
+  const int stages = R * S * (Cin / 128);
+  const size_t t128 = ((P + 127) / 128) * (size_t)(Cout / 128);
+  if (Cout % 128 == 0 && t128 >= (size_t)cus) return launch_rounds(t128, cus) * (4.0 + 0.69 * stages);
+  const size_t t64 = ((P + 63) / 64) * (size_t)(Cout / 64);
+  const int ks = conv_ksplit(t64, stages, 4, P * Cout, cus, work_bytes);
+  return launch_rounds(t64 * ks, cus) * (2.5 + 0.41 * stages / ks) + (ks > 1 ? 3.0 : 0.0);
+}
+
+// The kernel choice is made for a 256-CU device (MI355X) whatever the
+// context's CU count, so miaie_plan_conv2d_i8 (no context) and every launch
+// agree; the tile choices within one kernel use the context's CU count.
+constexpr int CONV_PLAN_CUS = 256;
+
 int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad, bool aligned16,
                       bool shifts_aligned4) {
   const int Ho = (H + 2 * pad - R) / stride + 1;
@@ -489,30 +542,30 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
                        (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31) &&
                        (size_t)Cout * R * S * Cin < ((size_t)1 << 31) && Cout / 32 <= 65535;
   if (rows_ok) return MIAIE_CONV_ROWS;
+  // The same kernel over 64-channel chunks of a deeper Cin (the rounding
+  // term in the accumulator start needs 9 * Cin * 2^14 < 2^30).
+  const bool deep_ok = stride == 1 && R == 3 && S == 3 && Cin % 64 == 0 && Cin <= 4096 && Cout % 32 == 0 &&
+                       aligned16 && shifts_aligned4 && N <= 65535 &&
+                       (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31) &&
+                       (size_t)Cout * R * S * Cin < ((size_t)1 << 31) && Cout / 32 <= 65535;
   // LDS-staged taps kernel (Cin a multiple of 128, Cout of 64): 32-bit copy
   // offsets, so X and W each stay below 2^31 bytes; 4-byte shift loads.
   const bool taps_ok = Cin % 128 == 0 && Cout % 64 == 0 && aligned16 && shifts_aligned4 &&
                        (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)Cout * R * S * Cin < ((size_t)1 << 31) &&
                        P < ((size_t)1 << 31) && Cout / 64 <= 65535;
+  if (deep_ok && taps_ok) {
+    const int nj = rows_deep_nj(N, Ho, Wo, Cin, Cout, CONV_PLAN_CUS);
+    return rows_deep_us(N, Ho, Wo, Cin, Cout, nj, CONV_PLAN_CUS) <=
+                   taps_us(P, Cin, Cout, R, S, CONV_PLAN_CUS, MIAIE_CTX_WORK_BYTES)
+               ? MIAIE_CONV_ROWS_DEEP
+               : MIAIE_CONV_TAPS;
+  }
+  if (deep_ok) return MIAIE_CONV_ROWS_DEEP;
   if (taps_ok) return MIAIE_CONV_TAPS;
   const bool fast = Cin % 32 == 0 && Cout % COB == 0 && aligned16 && P < ((size_t)1 << 31) &&
                     (P + PIX - 1) / PIX < ((size_t)1 << 31) && Cout / COB <= 65535;
   if (fast) return MIAIE_CONV_IGEMM;
   return MIAIE_CONV_DIRECT;
-}
-
-// Workgroups per tile of the implicit-GEMM kernel (1: no split).  Split when
-// at least 3 workgroups per tile fit on the CUs (a 2-way split measured no
-// faster: the reduce kernel's launch costs what the halved k-chain saves),
-// into at most 8 and at most cus / tiles parts, each keeping at least one
-// batch of loads per wave (4 * BATCH k-steps), with the partial sums inside
-// the context's workspace.
-static int conv_ksplit(size_t tiles, int T, int min_per_split, size_t elems, const miaie_ctx* ctx) {
-  if (tiles * 3 > (size_t)ctx->cus) return 1;
-  int ks = (int)std::min<size_t>((size_t)ctx->cus / tiles, 8);
-  ks = std::min(ks, T / min_per_split);
-  while (ks > 1 && (size_t)ks * elems * sizeof(int32_t) > ctx->work_bytes) --ks;
-  return ks > 1 ? ks : 1;
 }
 
 int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y,
@@ -527,13 +580,21 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
     if (Cin == 64) return launch_rows<64>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
     return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
   }
+  if (kernel == MIAIE_CONV_ROWS_DEEP) {
+    if (rows_deep_nj(N, Ho, Wo, Cin, Cout, ctx->cus) == 2)
+      conv::launch_rowsk_as<4, 64, 2>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout, pad, Ho, Wo);
+    else
+      conv::launch_rowsk_as<4, 32, 1>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout, pad, Ho, Wo);
+    return check_launch(ctx, "conv2d_i8_rowsk");
+  }
   if (kernel == MIAIE_CONV_TAPS) {
     // 128 x 128 tiles when they fill at least one round of CUs, else 64 x 64
     // (split over k when even those leave most CUs idle)
     const bool big = Cout % 128 == 0 && ((P + 127) / 128) * (size_t)(Cout / 128) >= (size_t)ctx->cus;
     const int tp = big ? 128 : 64;
     const unsigned pxb = (unsigned)((P + tp - 1) / tp), chb = (unsigned)(Cout / tp);
-    const int ks = big ? 1 : conv_ksplit((size_t)pxb * chb, R * S * (Cin / 128), 4, P * Cout, ctx);
+    const int ks = big ? 1 : conv_ksplit((size_t)pxb * chb, R * S * (Cin / 128), 4, P * Cout, ctx->cus,
+                                             ctx->work_bytes);
     auto go = [&](auto kernel, unsigned z, int32_t* psum) {
       hipLaunchKernelGGL(kernel, dim3(pxb, chb, z), dim3(256), 0, ctx->stream, X, W, shifts, Y, psum, N, H, Wd, Cin,
                          Cout, R, S, stride, pad, Ho, Wo, (int)z);
@@ -556,7 +617,7 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
   }
   if (kernel == MIAIE_CONV_IGEMM) {
     const unsigned pxb = (unsigned)((P + PIX - 1) / PIX), chb = (unsigned)(Cout / COB);
-    const int ks = conv_ksplit((size_t)pxb * chb, R * S * (Cin / 32), 4 * BATCH, P * Cout, ctx);
+    const int ks = conv_ksplit((size_t)pxb * chb, R * S * (Cin / 32), 4 * BATCH, P * Cout, ctx->cus, ctx->work_bytes);
     if (ks > 1) {
       int32_t* const part = static_cast<int32_t*>(ctx->work);
       hipLaunchKernelGGL(conv2d_i8_igemm<true>, dim3(pxb, chb, (unsigned)ks), dim3(256), 0, ctx->stream, X, W,

@@ -135,6 +135,7 @@ MIAIE_API int miaie_plan_set_cus(miaie_ctx* ctx, int cus, int* previous);
 #define MIAIE_CONV_IGEMM 1  /* implicit-GEMM kernel: Cin % 32 == 0, Cout % 64 == 0 */
 #define MIAIE_CONV_DIRECT 2 /* any shape, one thread per output element */
 #define MIAIE_CONV_TAPS 3   /* LDS-staged implicit GEMM over filter taps: Cin % 128 == 0, Cout % 64 == 0 */
+#define MIAIE_CONV_ROWS_DEEP 4 /* row-block kernel over 64-channel chunks of Cin: 3x3, stride 1, Cin % 64 == 0 up to 4096, Cout % 32 == 0 */
 MIAIE_API int miaie_plan_conv2d_i8(int N, int H, int W, int Cin, int Cout, int R, int S, int stride, int pad,
                                    int* kernel);
 
@@ -230,11 +231,14 @@ MIAIE_API int miaie_gemm_bf16_f32(miaie_ctx* ctx, const uint16_t* A, const uint1
  * (a device array the library cannot check: other values give unspecified
  * results), Y[N][Ho][Wo][Cout] with Ho = (H + 2*pad - R)/stride + 1 (Wo
  * alike).  Any shape: 3x3 stride-1 convolutions with Cin 32, 64 or 128 and
- * Cout a multiple of 32 take the row-block kernel; Cin a multiple of 128
- * with Cout a multiple of 64 the LDS-staged taps kernel; Cin a multiple of
- * 32 with Cout a multiple of 64 the implicit-GEMM kernel (the last two split
- * K over workgroups for small grids, through the context's workspace);
- * everything else a direct kernel (miaie_plan_conv2d_i8 reports which).
+ * Cout a multiple of 32 take the row-block kernel, and with another Cin
+ * that is a multiple of 64 (up to 4096) the row-block kernel over
+ * 64-channel chunks, or the taps kernel where its estimated time is lower;
+ * Cin a multiple of 128 with Cout a multiple of 64 the LDS-staged taps
+ * kernel; Cin a multiple of 32 with Cout a multiple of 64 the implicit-GEMM
+ * kernel (the last two split K over workgroups for small grids, through the
+ * context's workspace); everything else a direct kernel
+ * (miaie_plan_conv2d_i8 reports which).
  * R*S*Cin above 2^30 or N*H*W*Cin above 2^40 return MIAIE_EINVAL. */
 MIAIE_API int miaie_conv2d_i8_nhwc(miaie_ctx* ctx, const int8_t* X, const int8_t* W,
                                    const uint8_t* shifts, int8_t* Y, int N, int H, int W_, int Cin,

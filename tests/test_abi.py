@@ -91,12 +91,22 @@ def test_conv_planner_keeps_32_bit_offsets_in_range():
     assert mi.plan_conv2d_i8(n_big, 56, 56, 64, 64) == "igemm"
     assert mi.plan_conv2d_i8(2, 56, 56, 64, 64, stride=2) == "igemm"
     assert mi.plan_conv2d_i8(1, 5, 5, 4, 8) == "direct"
-    # deep layers (Cin a multiple of 128 above 128) and strided ones take the LDS-staged taps kernel
-    assert mi.plan_conv2d_i8(8, 14, 14, 256, 256) == "taps"
-    assert mi.plan_conv2d_i8(8, 7, 7, 512, 512) == "taps"
+    # deep 3x3 stride-1 layers: the chunked row-block kernel or the taps
+    # kernel, whichever the launch-time estimate favours; strided ones: taps
+    assert mi.plan_conv2d_i8(8, 14, 14, 256, 256) == "rows_deep"
+    assert mi.plan_conv2d_i8(8, 56, 56, 256, 256) == "rows_deep"
+    assert mi.plan_conv2d_i8(8, 28, 28, 512, 512) == "rows_deep"
+    assert mi.plan_conv2d_i8(8, 56, 56, 192, 96) == "rows_deep"          # Cin not a multiple of 128
+    assert mi.plan_conv2d_i8(8, 7, 7, 512, 512) == "taps"                # 56 tiles split 4 ways
+    assert mi.plan_conv2d_i8(32, 28, 28, 512, 512) == "taps"             # 784 tiles of 128 x 128
+    assert mi.plan_conv2d_i8(1, 3, 3, 4032, 64) == "rows_deep"
+    assert mi.plan_conv2d_i8(1, 3, 3, 4160, 64) == "igemm"               # above the 4096 bound, not a multiple of 128
+    assert mi.plan_conv2d_i8(8, 56, 56, 256, 256, 5, 5, 1, 2) == "taps"  # not 3x3
     assert mi.plan_conv2d_i8(8, 112, 112, 128, 128) == "rows"              # rows wider than 64: column blocks
     assert mi.plan_conv2d_i8(8, 112, 112, 128, 128, stride=2) == "taps"     # stride 2: not the row-block kernel
     n_deep = (1 << 31) // (14 * 14 * 256) + 1                             # X reaches 2^31 bytes
     assert mi.plan_conv2d_i8(n_deep, 14, 14, 256, 256) == "igemm"
+    big_deep = (1 << 31) // (9 * 256)                                     # weights reach 2^31 bytes
+    assert mi.plan_conv2d_i8(1, 1, 1, 256, big_deep + 64 - big_deep % 64) == "igemm"
     with pytest.raises(mi.MiaieError):
         mi.plan_conv2d_i8(1, 2, 2, 4, 4, 5, 5, 1, 0)                  # filter larger than the input

@@ -294,13 +294,16 @@ CONV_SHAPES = [
     (2, 7, 28, 128, 128, 3, 3, 1, 1),  # row-block 2 x 64 at Cin 128 (108 KiB of LDS), odd Ho
     (1, 6, 60, 128, 96, 3, 3, 1, 2),  # row-block 4 x 32 at Cin 128, pad 2
     (1, 5, 9, 96, 64, 3, 3, 1, 1),    # Cin 96: implicit-GEMM kernel
-    (1, 8, 8, 256, 64, 3, 3, 1, 1),   # taps kernel (LDS-staged), one tile split 3 ways over k (partials + reduce)
+    (1, 8, 8, 256, 64, 3, 3, 1, 1),   # chunked row-block kernel: four 64-channel chunks, one workgroup
+    (1, 16, 16, 256, 64, 3, 3, 2, 1),  # taps kernel (LDS-staged), stride 2: one tile split 4 ways over k (partials + reduce)
     (2, 7, 7, 512, 128, 3, 3, 1, 1),  # taps: 4 tiles split 8 ways, the last pixel block partial
     (1, 6, 6, 320, 64, 3, 3, 2, 1),   # Cin 320: implicit GEMM, stride 2, split over k
-    (1, 5, 70, 128, 64, 3, 3, 1, 1),  # taps: rows wider than 64 (left and right padding), not split
+    (1, 5, 70, 128, 64, 3, 3, 1, 1),  # row-block kernel at Cin 128, rows wider than 64: two column blocks
+    (1, 5, 70, 128, 64, 5, 5, 1, 2),  # taps, 5x5: pixel tiles across rows (left and right padding)
     (1, 9, 9, 128, 128, 3, 3, 2, 1),  # taps, stride 2
-    (8, 14, 14, 256, 256, 3, 3, 1, 1),  # deep CNN layer on taps: 100 tiles, not split (fewer than 3 workgroups per tile fit)
+    (8, 14, 14, 256, 256, 3, 3, 1, 1),  # deep CNN layer on the chunked row-block kernel (32 x 32 waves, 256 workgroups)
     (8, 7, 7, 512, 512, 3, 3, 1, 1),    # deepest, on taps: 56 tiles, split 4 ways
+    (2, 6, 70, 192, 96, 3, 3, 1, 1),  # chunked row-block: 3 chunks (odd), Cout 96 (4 rows x 32), two column blocks
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # fallback kernel (channels not multiples of 32/64)
     (2, 6, 7, 3, 5, 3, 3, 2, 0),      # fallback kernel
 ]
@@ -328,7 +331,7 @@ def _random_conv_cases(n=16, seed=1202):
     rng = np.random.default_rng(seed)
     cases = []
     for _ in range(n):
-        Cin = int(rng.choice([3, 32, 64, 96, 128, 256, 384]))
+        Cin = int(rng.choice([3, 32, 64, 96, 128, 192, 256, 320, 384]))
         Cout = int(rng.choice([8, 32, 64, 96, 128, 192, 256]))
         R = int(rng.choice([1, 3, 3, 3, 5]))
         stride = int(rng.choice([1, 1, 2]))
@@ -342,7 +345,7 @@ def _random_conv_cases(n=16, seed=1202):
 
 @pytest.mark.parametrize("shape", _random_conv_cases())
 def test_conv2d_i8_random_shapes(ctx, shape):
-    """Seeded random shapes over all four conv kernels (whichever the planner
+    """Seeded random shapes over the conv kernels (whichever the planner
     picks), shifts over [0, 31], bit-exact against the oracle."""
     N, H, W, Cin, Cout, R, S, stride, pad = shape
     _say("conv2d random", shape, mi.plan_conv2d_i8(N, H, W, Cin, Cout, R, S, stride, pad))
@@ -360,8 +363,8 @@ def test_conv2d_i8_random_shapes(ctx, shape):
 
 
 @pytest.mark.parametrize("shape", [
-    (1, 9, 70, 256, 128, 3, 3, 1, 1),   # 5 pixel tiles, the last partial
-    (2, 7, 7, 256, 256, 3, 3, 1, 1),    # one partial pixel tile, two channel tiles
+    (1, 9, 70, 256, 128, 3, 3, 2, 1),   # stride 2: 2 pixel tiles, the last partial
+    (2, 7, 7, 256, 256, 5, 5, 1, 2),    # 5x5: one partial pixel tile, two channel tiles
     (1, 17, 17, 128, 256, 3, 3, 2, 1),  # stride 2
     (1, 6, 6, 384, 128, 3, 3, 1, 0),    # no padding, three 128-channel chunks per tap
 ])
@@ -390,13 +393,54 @@ def test_conv2d_i8_taps_128_tiles(ctx, shape):
     assert np.array_equal(Yg, oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad))
 
 
+@pytest.mark.parametrize("shape,cus", [
+    ((1, 8, 8, 256, 128, 3, 3, 1, 1), 256),   # 32 x 32 waves (more workgroups)
+    ((1, 8, 8, 256, 128, 3, 3, 1, 1), 1),     # 32 x 64 waves (two MFMAs per pixel fragment)
+    ((2, 6, 70, 192, 128, 3, 3, 1, 0), 1),    # 3 chunks, two column blocks, no padding, 32 x 64 waves
+    ((16, 5, 9, 320, 128, 3, 3, 1, 1), 1),    # 5 chunks, image-per-XCD grid over 16 images, 32 x 64 waves
+    ((1, 2, 10, 256, 64, 3, 3, 1, 1), 256),   # fewer output rows than a row block
+    ((1, 3, 3, 4032, 64, 3, 3, 1, 1), 256),   # 63 chunks: Cin near the 4096 bound of the rounding term
+])
+@pytest.mark.parametrize("extreme", [False, True])
+def test_conv2d_i8_rows_deep(ctx, shape, cus, extreme):
+    """The chunked row-block kernel (Cin a multiple of 64 above 128, 3x3,
+    stride 1): both wave tiles, odd and even chunk counts, column blocks, both
+    grid forms, shifts over [0, 31].  `extreme` fills X and W with -128, the
+    largest |acc| (9 * Cin * 2^14) on top of the rounding term."""
+    N, H, W, Cin, Cout, R, S, stride, pad = shape
+    _say("conv2d rows_deep", shape, cus, extreme)
+    assert mi.plan_conv2d_i8(N, H, W, Cin, Cout, R, S, stride, pad) == "rows_deep"
+    rng = np.random.default_rng(sum(shape) + cus + extreme)
+    if extreme:
+        X = np.full((N, H, W, Cin), -128, np.int8)
+        Wt = np.full((Cout, R, S, Cin), -128, np.int8)
+    else:
+        X = rng.integers(-128, 128, size=(N, H, W, Cin), dtype=np.int8)
+        Wt = rng.integers(-128, 128, size=(Cout, R, S, Cin), dtype=np.int8)
+    sh = rng.integers(0, 32, size=Cout, dtype=np.uint8)
+    sh[:3] = [0, 31, 7]
+    Ho = (H + 2 * pad - R) // stride + 1
+    Wo = (W + 2 * pad - S) // stride + 1
+    prev = ctx.plan_set_cus(cus)
+    try:
+        dX, dW, dS = ctx.upload(X), ctx.upload(Wt), ctx.upload(sh)
+        dY = ctx.empty((N, Ho, Wo, Cout), np.int8)
+        ctx.conv2d_i8_nhwc(dX, dW, dS, dY, N, H, W, Cin, Cout, R, S, stride, pad)
+        ctx.wait(60_000)
+        Yg = ctx.download(dY)
+    finally:
+        ctx.plan_set_cus(prev)
+    assert np.array_equal(Yg, oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad))
+
+
 @pytest.mark.parametrize("shape", [
     (1, 6, 56, 64, 64, 3, 3, 1, 1),   # row-block 2 rows x 64 channels
     (1, 5, 20, 32, 96, 3, 3, 1, 1),   # row-block 4 rows x 32 channels
     (1, 4, 24, 128, 64, 3, 3, 1, 1),  # row-block at Cin 128
     (1, 8, 8, 64, 64, 3, 3, 2, 1),    # implicit-GEMM kernel
-    (1, 8, 8, 256, 64, 3, 3, 1, 1),   # taps kernel split over k (requantize in the reduce kernel)
-    (1, 5, 70, 128, 64, 3, 3, 1, 1),  # taps kernel, requantize in its own epilogue
+    (1, 16, 16, 256, 64, 3, 3, 2, 1),  # taps kernel split over k (requantize in the reduce kernel)
+    (1, 56, 100, 128, 64, 1, 1, 1, 0),  # taps kernel, not split: requantize in its own epilogue
+    (1, 4, 20, 192, 96, 3, 3, 1, 1),  # chunked row-block kernel
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # direct kernel
 ])
 @pytest.mark.parametrize("small", [False, True])
