@@ -484,8 +484,8 @@ def extra_conv_shapes(ctx, timer, args) -> dict:
     import aiehlc_amd as mi
 
     out = {}
-    for N, H, Ci, Co in ((8, 112, 64, 64), (8, 112, 128, 128), (8, 56, 256, 256), (8, 14, 256, 256),
-                         (8, 7, 512, 512)):
+    for N, H, Ci, Co in ((8, 112, 64, 64), (8, 112, 128, 128), (8, 56, 256, 256), (8, 28, 512, 512),
+                         (8, 14, 256, 256), (8, 7, 512, 512)):
         dX, dW, dS, dY = (ctx.empty((N, H, H, Ci), np.int8), ctx.empty((Co, 3, 3, Ci), np.int8),
                           ctx.empty((Co,), np.uint8), ctx.empty((N, H, H, Co), np.int8))
         ctx.fill_i8(dX, N * H * H * Ci, 3)
