@@ -497,19 +497,31 @@ static int conv_ksplit(size_t tiles, int T, int min_per_split, size_t elems, int
 // chunk or per taps stage.
 static double launch_rounds(size_t wgs, int cus) { return (double)((wgs + cus - 1) / cus); }
 
-// conv2d_i8_rowsk<4, 32*nj, nj>: 8 waves of 32 pixels x 32*nj channels
-static double rows_deep_us(int N, int Ho, int Wo, int Cin, int Cout, int nj, int cus) {
-  const size_t wgs = (size_t)N * ((Ho + 3) / 4) * ((Wo + conv::PB - 1) / conv::PB) * (size_t)(Cout / (32 * nj));
+// conv2d_i8_rowsk<rows, 32*nj, nj, bw>: blocks of bw columns (64, or 32 for
+// narrow layers) x rows = 256/bw rows, 8 waves of 32 pixels x 32*nj channels
+struct RowsDeepTile {
+  int nj, bw;
+};
+static double rows_deep_us(int N, int Ho, int Wo, int Cin, int Cout, RowsDeepTile t, int cus) {
+  const int rows = 256 / t.bw;
+  const size_t wgs = (size_t)N * ((Ho + rows - 1) / rows) * ((Wo + t.bw - 1) / t.bw) * (size_t)(Cout / (32 * t.nj));
   const int nk = Cin / 64;
-  return launch_rounds(wgs, cus) * (nj == 2 ? 3.5 + 1.68 * nk : 2.8 + 1.0 * nk);
+  return launch_rounds(wgs, cus) * (t.nj == 2 ? 3.5 + 1.68 * nk : 2.8 + 1.0 * nk);
 }
 
-// Wave tile of the chunked row-block kernel: 32 x 64 (two MFMAs per pixel
-// fragment, 3/4 of the LDS reads per MAC) unless it leaves so few workgroups
-// that 32 x 32 finishes first.
-static int rows_deep_nj(int N, int Ho, int Wo, int Cin, int Cout, int cus) {
-  if (Cout % 64) return 1;
-  return rows_deep_us(N, Ho, Wo, Cin, Cout, 2, cus) <= rows_deep_us(N, Ho, Wo, Cin, Cout, 1, cus) ? 2 : 1;
+// Tile of the chunked row-block kernel with the lowest estimate: 32 x 64
+// waves (two MFMAs per pixel fragment, 3/4 of the LDS reads per MAC) unless
+// they leave so few workgroups that 32 x 32 finishes first; 32-column blocks
+// where 64 would leave most columns empty (Wo <= 32, or just above 64).
+static RowsDeepTile rows_deep_tile(int N, int Ho, int Wo, int Cin, int Cout, int cus) {
+  RowsDeepTile best{1, 64};
+  double best_us = rows_deep_us(N, Ho, Wo, Cin, Cout, best, cus);
+  for (RowsDeepTile t : {RowsDeepTile{2, 64}, RowsDeepTile{2, 32}, RowsDeepTile{1, 32}}) {
+    if (t.nj == 2 && Cout % 64) continue;
+    const double us = rows_deep_us(N, Ho, Wo, Cin, Cout, t, cus);
+    if (us < best_us) best = t, best_us = us;
+  }
+  return best;
 }
 
 // conv2d_i8_taps as its launcher runs it: 128 x 128 tiles when they fill a
@@ -554,8 +566,8 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
                        (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)Cout * R * S * Cin < ((size_t)1 << 31) &&
                        P < ((size_t)1 << 31) && Cout / 64 <= 65535;
   if (deep_ok && taps_ok) {
-    const int nj = rows_deep_nj(N, Ho, Wo, Cin, Cout, CONV_PLAN_CUS);
-    return rows_deep_us(N, Ho, Wo, Cin, Cout, nj, CONV_PLAN_CUS) <=
+    const RowsDeepTile t = rows_deep_tile(N, Ho, Wo, Cin, Cout, CONV_PLAN_CUS);
+    return rows_deep_us(N, Ho, Wo, Cin, Cout, t, CONV_PLAN_CUS) <=
                    taps_us(P, Cin, Cout, R, S, CONV_PLAN_CUS, MIAIE_CTX_WORK_BYTES)
                ? MIAIE_CONV_ROWS_DEEP
                : MIAIE_CONV_TAPS;
@@ -581,10 +593,15 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
     return launch_rows<32>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
   }
   if (kernel == MIAIE_CONV_ROWS_DEEP) {
-    if (rows_deep_nj(N, Ho, Wo, Cin, Cout, ctx->cus) == 2)
-      conv::launch_rowsk_as<4, 64, 2>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout, pad, Ho, Wo);
+    const RowsDeepTile t = rows_deep_tile(N, Ho, Wo, Cin, Cout, ctx->cus);
+    if (t.bw == 64 && t.nj == 2)
+      conv::launch_rowsk_as<4, 64, 2, 64>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout, pad, Ho, Wo);
+    else if (t.bw == 64)
+      conv::launch_rowsk_as<4, 32, 1, 64>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout, pad, Ho, Wo);
+    else if (t.nj == 2)
+      conv::launch_rowsk_as<8, 64, 2, 32>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout, pad, Ho, Wo);
     else
-      conv::launch_rowsk_as<4, 32, 1>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout, pad, Ho, Wo);
+      conv::launch_rowsk_as<8, 32, 1, 32>(ctx->stream, X, W, shifts, Y, N, H, Wd, Cin, Cout, pad, Ho, Wo);
     return check_launch(ctx, "conv2d_i8_rowsk");
   }
   if (kernel == MIAIE_CONV_TAPS) {

@@ -47,28 +47,30 @@ __device__ __forceinline__ int xswz(int col) {
   return (col * CIN / 256) & (CIN / 16 - 1);
 }
 
-template <int R, int S, int CIN, int ROWS, int WCO>
+// BW: output columns per block (64, or 32 for narrow layers).
+template <int R, int S, int CIN, int ROWS, int WCO, int BW = PB>
 struct RowsGeom {
   static_assert(ROWS * WCO % 128 == 0 && WCO % 32 == 0, "8 waves of 32 pixels x 32 channels (or a multiple)");
   static constexpr int NWC = WCO / 32;                      // 32-channel blocks per workgroup
-  static constexpr int XR = ROWS + R - 1, XC = PB + S - 1;  // staged input rows / columns
+  static constexpr int XR = ROWS + R - 1, XC = BW + S - 1;  // staged input rows / columns
   static constexpr int NCH = CIN / 16;                      // 16-byte chunks per pixel
-  // X staging map: one pass covers RPP whole rows of the first PB staged
-  // columns (thread -> chunk tid % NCH of column tid / NCH % PB), XQ passes
+  static constexpr int BW_ = BW;
+  // X staging map: one pass covers RPP whole rows of the first BW staged
+  // columns (thread -> chunk tid % NCH of column tid / NCH % BW), XQ passes
   // cover the XR rows, and one more load per thread (the first XE threads)
   // covers the last S - 1 columns of every row.
-  static constexpr int RPP = 512 / (PB * NCH);              // rows per pass
+  static constexpr int RPP = 512 / (BW * NCH);              // rows per pass
   static constexpr int XQ = (XR + RPP - 1) / RPP;           // passes
-  static constexpr int XE = XR * (XC - PB) * NCH;           // chunks of the last S - 1 columns
+  static constexpr int XE = XR * (XC - BW) * NCH;           // chunks of the last S - 1 columns
   static constexpr int RSC = R * S * CIN, WP = RSC + 16;    // weight row length / LDS pitch
   static constexpr int WTOT = WCO * RSC / 16;               // W chunks
   static constexpr int WQ = (WTOT + 511) / 512;
   static constexpr int WREM = WTOT - 512 * (WQ - 1);        // W chunks of the last pass
-  static_assert(512 % (PB * NCH) == 0 && XE <= 512, "row-block conv staging map");
+  static_assert(512 % (BW * NCH) == 0 && XE <= 512, "row-block conv staging map");
   static constexpr int X_BYTES = XR * XC * CIN;
   static constexpr int W_BYTES = WCO * WP;
   static constexpr int YP = WCO + 16;                       // LDS pitch of one staged output pixel
-  static constexpr int Y_BYTES = ROWS * PB * YP;
+  static constexpr int Y_BYTES = ROWS * BW * YP;
   static constexpr int LDS = X_BYTES + W_BYTES + Y_BYTES;
   static constexpr int T = R * S * CIN / 32;                // 32-wide k-steps
   static_assert(LDS <= 163840, "row-block conv LDS budget (160 KiB per workgroup on gfx950)");
@@ -87,7 +89,7 @@ __device__ __forceinline__ void rows_epilogue(const v16i& acc, const uint32_t (&
                                               int rr, int pb, int wc, int fr, int fh, int lane, int n, int ho0,
                                               int wc0, int co0, int Ho, int Wo, int Cout, int8_t* __restrict__ Y) {
   const int px = 32 * pb + fr;
-  int8_t* const yl = ys + (rr * PB + px) * G::YP + 32 * wc + 4 * fh;
+  int8_t* const yl = ys + (rr * G::BW_ + px) * G::YP + 32 * wc + 4 * fh;
   if (hi_form) {
     // every shift of the wave >= 8: y is the high byte of
     // sat_int16(acc >> (s - 8)) (floor shifts compose; saturating at 16 bits
@@ -118,7 +120,7 @@ __device__ __forceinline__ void rows_epilogue(const v16i& acc, const uint32_t (&
   __builtin_amdgcn_wave_barrier();
   const int sp = 32 * pb + (lane >> 1), sh = lane & 1;
   if (wc0 + sp < Wo && ho0 + rr < Ho) {
-    const v4i v = *reinterpret_cast<const v4i*>(ys + (rr * PB + sp) * G::YP + 32 * wc + 16 * sh);
+    const v4i v = *reinterpret_cast<const v4i*>(ys + (rr * G::BW_ + sp) * G::YP + 32 * wc + 16 * sh);
     *reinterpret_cast<v4i*>(Y + (uint32_t)(((n * Ho + ho0 + rr) * Wo + wc0 + sp) * Cout + co0 + 32 * wc + 16 * sh)) = v;
   }
 }
@@ -285,8 +287,9 @@ inline void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, con
 
 // Row-block kernel over input-channel chunks, for 3x3 stride-1 layers whose
 // Cin (a multiple of CK = 64) is too deep to stage whole.  The workgroup
-// owns an output block as conv2d_i8_rows does (ROWS rows x 64 columns x WCO
-// channels), its 8 waves each 32 pixels x 32*NJ channels (NJ MFMAs share
+// owns an output block as conv2d_i8_rows does (ROWS rows x BW columns x WCO
+// channels; BW = 32 for narrow layers), its 8 waves each 32 pixels x 32*NJ
+// channels (NJ MFMAs share
 // each X fragment, so NJ = 2 reads 3/4 of the LDS bytes per MAC of NJ = 1),
 // and walks Cin in chunks of 64 channels: each chunk stages what
 // conv2d_i8_rows<3,3,64> stages for its whole input (the ROWS+2 padded input
@@ -298,17 +301,18 @@ inline void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, con
 // chunk suffices.  Offsets are 32-bit
 // from the tensor base (X, W and Y below 2^31 bytes), and the accumulators
 // start at the rounding term: |acc| <= 9*Cin*2^14 < 2^30 for Cin <= 4096.
-template <int ROWS, int WCO, int NJ>
+template <int ROWS, int WCO, int NJ, int BW>
 __global__ __launch_bounds__(512) void conv2d_i8_rowsk(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
                                                        const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
                                                        int H, int Wd, int Cin, int Cout, int pad, int Ho, int Wo,
                                                        int xg, int ncb) {
   constexpr int CK = 64;
-  using G = RowsGeom<3, 3, CK, ROWS, WCO>;
+  using G = RowsGeom<3, 3, CK, ROWS, WCO, BW>;
   constexpr int BUF = G::X_BYTES + G::W_BYTES;  // one chunk's X and W
   constexpr int WPC = 9 * CK / 16;              // 16-byte W chunks per output channel per input chunk
   static_assert(2 * BUF + G::Y_BYTES <= 163840, "chunked row-block conv LDS budget");
-  static_assert(ROWS * 2 * (WCO / (32 * NJ)) == 8, "8 waves of 32 pixels x 32*NJ channels");
+  constexpr int NPB = BW / 32;  // 32-pixel halves of a block row
+  static_assert(ROWS * NPB * (WCO / (32 * NJ)) == 8, "8 waves of 32 pixels x 32*NJ channels");
   __shared__ __attribute__((aligned(16))) int8_t smem[2 * BUF + G::Y_BYTES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, fh = lane >> 5;
@@ -327,14 +331,14 @@ __global__ __launch_bounds__(512) void conv2d_i8_rowsk(const int8_t* __restrict_
   if (ncb > 1) {
     const int cbk = rb % ncb;
     rb /= ncb;
-    wc0 = cbk * PB;
+    wc0 = cbk * BW;
   }
   const int ho0 = rb * ROWS;
   const int co0 = cb * WCO;
   int8_t* const ys = smem + 2 * BUF;
   // wave: output row rr, pixels 32pb .. +32, channels 32*NJ*wj .. +32*NJ
   constexpr int NWJ = WCO / (32 * NJ);
-  const int wj = wave % NWJ, pb = (wave / NWJ) & 1, rr = wave / (2 * NWJ);
+  const int wj = wave % NWJ, pb = (wave / NWJ) % NPB, rr = wave / (NPB * NWJ);
 
   // Staging map of conv2d_i8_rows<3,3,64>, with each source offset computed
   // once; chunk kc adds kc * CK.  Positions outside the image load the
@@ -342,9 +346,9 @@ __global__ __launch_bounds__(512) void conv2d_i8_rowsk(const int8_t* __restrict_
   // are 64-bit: formed in 32 bits, each became a v_mad_u64_u32 whose unused
   // high addend half the compiler took from any register, at times one still
   // waiting for a load, so the next load waited for it.
-  const int xc = tid % G::NCH, xcol = (tid / G::NCH) % PB, xrow = tid / (G::NCH * PB);
+  const int xc = tid % G::NCH, xcol = (tid / G::NCH) % BW, xrow = tid / (G::NCH * BW);
   const int et = tid % G::XE;
-  const int ec = et % G::NCH, ecol = PB + (et / G::NCH) % (G::XC - PB), erow = et / (G::NCH * (G::XC - PB));
+  const int ec = et % G::NCH, ecol = BW + (et / G::NCH) % (G::XC - BW), erow = et / (G::NCH * (G::XC - BW));
   auto x_src = [&](int row, int col, int c, bool& in) -> uint64_t {
     const int hi = ho0 + row - pad, wi = wc0 + col - pad;
     in = (unsigned)hi < (unsigned)H && (unsigned)wi < (unsigned)Wd;
@@ -456,14 +460,14 @@ __global__ __launch_bounds__(512) void conv2d_i8_rowsk(const int8_t* __restrict_
 
 // Grid and launch of the chunked row-block kernel (shapes already checked by
 // the caller: deep_ok in conv2d_kernel_for).
-template <int ROWS, int WCO, int NJ>
+template <int ROWS, int WCO, int NJ, int BW>
 inline void launch_rowsk_as(hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
                             int H, int Wd, int Cin, int Cout, int pad, int Ho, int Wo) {
-  const int ncb = (Wo + PB - 1) / PB;
+  const int ncb = (Wo + BW - 1) / BW;
   const unsigned rbs = (unsigned)((Ho + ROWS - 1) / ROWS * ncb), cbs = (unsigned)(Cout / WCO);
   const bool by_xcd = N % 8 == 0 && rbs <= 65535 && (size_t)(N / 8) * cbs <= 65535;
   const dim3 grid = by_xcd ? dim3(8, rbs, (unsigned)(N / 8) * cbs) : dim3(rbs, cbs, (unsigned)N);
-  hipLaunchKernelGGL((conv2d_i8_rowsk<ROWS, WCO, NJ>), grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd, Cin, Cout, pad, Ho,
+  hipLaunchKernelGGL((conv2d_i8_rowsk<ROWS, WCO, NJ, BW>), grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd, Cin, Cout, pad, Ho,
                      Wo, by_xcd ? N / 8 : 0, ncb);
 }
 

@@ -98,7 +98,8 @@ def test_conv_planner_keeps_32_bit_offsets_in_range():
     assert mi.plan_conv2d_i8(8, 28, 28, 512, 512) == "rows_deep"
     assert mi.plan_conv2d_i8(8, 56, 56, 192, 96) == "rows_deep"          # Cin not a multiple of 128
     assert mi.plan_conv2d_i8(8, 7, 7, 512, 512) == "taps"                # 56 tiles split 4 ways
-    assert mi.plan_conv2d_i8(32, 28, 28, 512, 512) == "taps"             # 784 tiles of 128 x 128
+    assert mi.plan_conv2d_i8(32, 28, 28, 512, 512) == "rows_deep"        # 32-column blocks
+    assert mi.plan_conv2d_i8(32, 28, 28, 512, 512, 1, 1, 1, 0) == "taps"  # 1x1: not the row-block kernel
     assert mi.plan_conv2d_i8(1, 3, 3, 4032, 64) == "rows_deep"
     assert mi.plan_conv2d_i8(1, 3, 3, 4160, 64) == "igemm"               # above the 4096 bound, not a multiple of 128
     assert mi.plan_conv2d_i8(8, 56, 56, 256, 256, 5, 5, 1, 2) == "taps"  # not 3x3

@@ -394,10 +394,12 @@ def test_conv2d_i8_taps_128_tiles(ctx, shape):
 
 
 @pytest.mark.parametrize("shape,cus", [
-    ((1, 8, 8, 256, 128, 3, 3, 1, 1), 256),   # 32 x 32 waves (more workgroups)
-    ((1, 8, 8, 256, 128, 3, 3, 1, 1), 1),     # 32 x 64 waves (two MFMAs per pixel fragment)
-    ((2, 6, 70, 192, 128, 3, 3, 1, 0), 1),    # 3 chunks, two column blocks, no padding, 32 x 64 waves
+    ((1, 8, 8, 256, 128, 3, 3, 1, 1), 256),   # 32 x 32 waves (more workgroups), 64-column blocks
+    ((1, 8, 8, 256, 128, 3, 3, 1, 1), 1),     # 32 x 64 waves (two MFMAs per pixel fragment), 32-column blocks
+    ((2, 6, 70, 192, 128, 3, 3, 1, 0), 1),    # 3 chunks, two 64-column blocks, no padding, 32 x 64 waves
     ((16, 5, 9, 320, 128, 3, 3, 1, 1), 1),    # 5 chunks, image-per-XCD grid over 16 images, 32 x 64 waves
+    ((2, 9, 20, 192, 128, 3, 3, 1, 1), 1),    # 8 rows x 32 columns, 32 x 64 waves, last row block partial
+    ((1, 9, 20, 256, 96, 3, 3, 1, 1), 1),     # 8 rows x 32 columns, 32 x 32 waves (Cout 96)
     ((1, 2, 10, 256, 64, 3, 3, 1, 1), 256),   # fewer output rows than a row block
     ((1, 3, 3, 4032, 64, 3, 3, 1, 1), 256),   # 63 chunks: Cin near the 4096 bound of the rounding term
 ])
