@@ -15,13 +15,19 @@
 //   seq_full_col    example/multi/seq_full_col.cpp:65-181 (8 stages, expects 23)
 //   vek385          example/multi/vek385_verification.cpp:104-157 (3x3 A.A per tile)
 //   gemm M N K s    int8 GEMM + requant (benchmark configs), golden on sampled rows
-//   conv [reps]     int8 3x3 conv2d, benchmark config 4, golden on one image;
-//                   with reps, then times reps back-to-back calls
+//   conv [reps] [streams]
+//                   int8 3x3 conv2d, benchmark config 4, golden on one image;
+//                   with reps, then times reps back-to-back calls; with
+//                   streams > 1, also reps independent calls dealt round-robin
+//                   over that many contexts (one stream and one set of
+//                   buffers each), every context's output checked against
+//                   the first's
 //   mlp M K F N     chained int8 MLP, golden on sampled rows
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -202,7 +208,7 @@ int run_gemm(miaie::Context& ctx, int M, int N, int K, int shift) {
   return report(mismatches, "gemm");
 }
 
-int run_conv(miaie::Context& ctx, int reps) {
+int run_conv(miaie::Context& ctx, int reps, int streams) {
   const int Nb = 8, H = 56, Wd = 56, C = 64, Co = 64;
   const std::vector<int8_t> X = seeded_i8((size_t)Nb * H * Wd * C, 3), W = seeded_i8((size_t)Co * 9 * C, 4);
   const std::vector<uint8_t> sh = seeded_shifts(Co, 7);
@@ -240,6 +246,43 @@ int run_conv(miaie::Context& ctx, int reps) {
     if (!ctx.wait(kDeadlineMs)) return 2;
     printf("conv2d back-to-back: %.3f us per call over %d calls\n", us_since(t0) / reps, reps);
   }
+  if (reps > 0 && streams > 1) {
+    // independent convolutions (a batch each) on `streams` contexts: the
+    // command processor's per-launch work of one stream overlaps another's
+    struct Set {
+      std::unique_ptr<miaie::Context> ctx;
+      miaie::Buffer<int8_t> X, W, Y;
+      miaie::Buffer<uint8_t> S;
+    };
+    std::vector<Set> sets;
+    for (int s = 0; s < streams; ++s) {
+      auto c = std::make_unique<miaie::Context>(0);
+      miaie::Context& cr = *c;
+      sets.push_back(Set{std::move(c), miaie::Buffer<int8_t>(cr, X.size()), miaie::Buffer<int8_t>(cr, W.size()),
+                         miaie::Buffer<int8_t>(cr, X.size()), miaie::Buffer<uint8_t>(cr, Co)});
+      sets.back().X.move_in(X);
+      sets.back().W.move_in(W);
+      sets.back().S.move_in(sh);
+    }
+    auto issue = [&]() {
+      for (int i = 0; i < reps; ++i) {
+        Set& st = sets[i % streams];
+        miaie::conv2d_i8(st.X, st.W, st.S, st.Y, miaie::ConvShape{Nb, H, Wd, C, Co}, *st.ctx);
+      }
+      for (Set& st : sets)
+        if (!st.ctx->wait(kDeadlineMs)) return false;
+      return true;
+    };
+    if (!issue()) return 2;
+    const auto t0 = clk::now();
+    if (!issue()) return 2;
+    printf("conv2d on %d streams: %.3f us per call over %d calls\n", streams, us_since(t0) / reps, reps);
+    const std::vector<int8_t> Y0 = dY.move_out();
+    for (Set& st : sets) mismatches += st.Y.move_out() != Y0;
+    // last constructed first, so each context hands "current" back to the
+    // one constructed before it
+    while (!sets.empty()) sets.pop_back();
+  }
   return report(mismatches, "conv2d");
 }
 
@@ -274,7 +317,7 @@ int run_mlp(miaie::Context& ctx, int M, int K, int F, int Nout) {
 int usage() {
   fprintf(stderr,
           "usage: miaie_examples mm [n 8|16] [base] | perf | nokernelload | multi_tile | seq_full_col | vek385 |\n"
-          "                      gemm M N K shift | conv [reps] | mlp M K F N\n");
+          "                      gemm M N K shift | conv [reps] [streams] | mlp M K F N\n");
   return 64;
 }
 
@@ -298,7 +341,7 @@ int main(int argc, char** argv) {
     if (cmd == "seq_full_col") return run_chain(ctx, std::vector<int32_t>(8, 1), 23, "seq_full_col");
     if (cmd == "vek385") return run_vek385(ctx);
     if (cmd == "gemm") return run_gemm(ctx, arg(2, 4096), arg(3, 4096), arg(4, 4096), arg(5, 10));
-    if (cmd == "conv") return run_conv(ctx, arg(2, 0));
+    if (cmd == "conv") return run_conv(ctx, arg(2, 0), arg(3, 1));
     if (cmd == "mlp") return run_mlp(ctx, arg(2, 256), arg(3, 4096), arg(4, 11008), arg(5, 4096));
     return usage();
   } catch (const miaie::Error& e) {

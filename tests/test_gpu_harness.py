@@ -21,6 +21,7 @@ CASES = [
     (["gemm", "4096", "4096", "4096", "10"], "CPU result matches"),
     (["gemm", "512", "384", "192", "9"], "CPU result matches"),
     (["conv"], "CPU result matches"),
+    (["conv", "200", "2"], "CPU result matches"),  # also two streams, each output against the first
     (["mlp", "256", "4096", "11008", "4096"], "CPU result matches"),
 ]
 
