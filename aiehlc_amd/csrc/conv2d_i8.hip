@@ -524,6 +524,14 @@ static RowsDeepTile rows_deep_tile(int N, int Ho, int Wo, int Cin, int Cout, int
   return best;
 }
 
+// conv2d_i8_rows<3,3,128,...> (118 KiB of LDS: one workgroup per CU), 3.57
+// us per workgroup (8x112x112x128 in 7 rounds, 25.0 us)
+static double rows128_us(int N, int Ho, int Wo, int Cout, int cus) {
+  const int rows = Cout % 64 == 0 ? 2 : 4, wco = Cout % 64 == 0 ? 64 : 32;
+  const size_t wgs = (size_t)N * ((Ho + rows - 1) / rows) * ((Wo + conv::PB - 1) / conv::PB) * (size_t)(Cout / wco);
+  return launch_rounds(wgs, cus) * 3.57;
+}
+
 // conv2d_i8_taps as its launcher runs it: 128 x 128 tiles when they fill a
 // round of CUs, else 64 x 64 split over k; a stage is one tap x 128 channels.
 static double taps_us(size_t P, int Cin, int Cout, int R, int S, int cus, size_t work_bytes) {
@@ -553,13 +561,23 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
                        aligned16 && shifts_aligned4 && N <= 65535 &&
                        (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31) &&
                        (size_t)Cout * R * S * Cin < ((size_t)1 << 31) && Cout / 32 <= 65535;
-  if (rows_ok) return MIAIE_CONV_ROWS;
   // The same kernel over 64-channel chunks of a deeper Cin (the rounding
   // term in the accumulator start needs 9 * Cin * 2^14 < 2^30).
   const bool deep_ok = stride == 1 && R == 3 && S == 3 && Cin % 64 == 0 && Cin <= 4096 && Cout % 32 == 0 &&
                        aligned16 && shifts_aligned4 && N <= 65535 &&
                        (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)N * Ho * Wo * Cout < ((size_t)1 << 31) &&
                        (size_t)Cout * R * S * Cin < ((size_t)1 << 31) && Cout / 32 <= 65535;
+  if (rows_ok) {
+    // At Cin = 128 both apply: the chunked kernel's 32-column blocks leave
+    // fewer empty columns on narrow layers, which pays where the row-block
+    // kernel's grid takes more than one round of CUs
+    if (Cin == 128 && deep_ok) {
+      const RowsDeepTile t = rows_deep_tile(N, Ho, Wo, Cin, Cout, CONV_PLAN_CUS);
+      if (rows_deep_us(N, Ho, Wo, Cin, Cout, t, CONV_PLAN_CUS) < rows128_us(N, Ho, Wo, Cout, CONV_PLAN_CUS))
+        return MIAIE_CONV_ROWS_DEEP;
+    }
+    return MIAIE_CONV_ROWS;
+  }
   // LDS-staged taps kernel (Cin a multiple of 128, Cout of 64): 32-bit copy
   // offsets, so X and W each stay below 2^31 bytes; 4-byte shift loads.
   const bool taps_ok = Cin % 128 == 0 && Cout % 64 == 0 && aligned16 && shifts_aligned4 &&

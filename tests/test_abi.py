@@ -104,6 +104,8 @@ def test_conv_planner_keeps_32_bit_offsets_in_range():
     assert mi.plan_conv2d_i8(1, 3, 3, 4160, 64) == "igemm"               # above the 4096 bound, not a multiple of 128
     assert mi.plan_conv2d_i8(8, 56, 56, 256, 256, 5, 5, 1, 2) == "taps"  # not 3x3
     assert mi.plan_conv2d_i8(8, 112, 112, 128, 128) == "rows"              # rows wider than 64: column blocks
+    assert mi.plan_conv2d_i8(8, 28, 28, 128, 128) == "rows"                # one round of row blocks
+    assert mi.plan_conv2d_i8(32, 28, 28, 128, 128) == "rows_deep"          # narrow, several rounds: 32-column blocks
     assert mi.plan_conv2d_i8(8, 112, 112, 128, 128, stride=2) == "taps"     # stride 2: not the row-block kernel
     n_deep = (1 << 31) // (14 * 14 * 256) + 1                             # X reaches 2^31 bytes
     assert mi.plan_conv2d_i8(n_deep, 14, 14, 256, 256) == "igemm"

@@ -304,6 +304,7 @@ CONV_SHAPES = [
     (8, 14, 14, 256, 256, 3, 3, 1, 1),  # deep CNN layer on the chunked row-block kernel (32 x 32 waves, 256 workgroups)
     (8, 7, 7, 512, 512, 3, 3, 1, 1),    # deepest, on taps: 56 tiles, split 4 ways
     (2, 6, 70, 192, 96, 3, 3, 1, 1),  # chunked row-block: 3 chunks (odd), Cout 96 (4 rows x 32), two column blocks
+    (32, 14, 14, 128, 128, 3, 3, 1, 1),  # Cin 128 on the chunked row-block kernel (narrow layer, several rounds)
     (1, 5, 5, 4, 8, 3, 3, 1, 1),      # fallback kernel (channels not multiples of 32/64)
     (2, 6, 7, 3, 5, 3, 3, 2, 0),      # fallback kernel
 ]
