@@ -289,18 +289,17 @@ inline void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, con
 // Cin (a multiple of CK = 64) is too deep to stage whole.  The workgroup
 // owns an output block as conv2d_i8_rows does (ROWS rows x BW columns x WCO
 // channels; BW = 32 for narrow layers), its 8 waves each 32 pixels x 32*NJ
-// channels (NJ MFMAs share
-// each X fragment, so NJ = 2 reads 3/4 of the LDS bytes per MAC of NJ = 1),
-// and walks Cin in chunks of 64 channels: each chunk stages what
-// conv2d_i8_rows<3,3,64> stages for its whole input (the ROWS+2 padded input
-// rows, 64 channels of them, and the WCO channels' 3x3x64 weights), into one
-// of two LDS buffers.  The next chunk's loads go out into registers before
-// the current chunk's 18*NJ MFMAs per wave run from the other buffer, and
-// are written to LDS one load at a time between the second half of those
-// MFMAs, so the writes run under the MFMAs and one workgroup barrier per
-// chunk suffices.  Offsets are 32-bit
-// from the tensor base (X, W and Y below 2^31 bytes), and the accumulators
-// start at the rounding term: |acc| <= 9*Cin*2^14 < 2^30 for Cin <= 4096.
+// channels (NJ MFMAs share each X fragment, so NJ = 2 reads 3/4 of the LDS
+// bytes per MAC of NJ = 1), and walks Cin in chunks of 64 channels: each
+// chunk stages what conv2d_i8_rows<3,3,64> stages for its whole input (the
+// ROWS+2 padded input rows, 64 channels of them, and the WCO channels'
+// 3x3x64 weights), into one of two LDS buffers.  The next chunk's loads go
+// out into registers before the current chunk's 18*NJ MFMAs per wave run
+// from the other buffer, and are written to LDS one load at a time between
+// the second half of those MFMAs, so the writes run under the MFMAs and one
+// workgroup barrier per chunk suffices.  The launcher keeps X, W and Y below
+// 2^31 bytes (the Y store offset is 32-bit), and the accumulators start at
+// the rounding term: |acc| <= 9*Cin*2^14 < 2^30 for Cin <= 4096.
 template <int ROWS, int WCO, int NJ, int BW>
 __global__ __launch_bounds__(512) void conv2d_i8_rowsk(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
                                                        const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
