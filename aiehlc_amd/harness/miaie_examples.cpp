@@ -243,8 +243,10 @@ int run_conv(miaie::Context& ctx, int reps, int streams) {
     if (!ctx.wait(kDeadlineMs)) return 2;
     const auto t0 = clk::now();
     for (int i = 0; i < reps; ++i) miaie::conv2d_i8(dX, dW, dS, dY, miaie::ConvShape{Nb, H, Wd, C, Co}, ctx);
+    const double issue_us = us_since(t0) / reps;  // the host's time per call alone
     if (!ctx.wait(kDeadlineMs)) return 2;
-    printf("conv2d back-to-back: %.3f us per call over %d calls\n", us_since(t0) / reps, reps);
+    printf("conv2d back-to-back: %.3f us per call over %d calls (host issue %.3f us per call)\n", us_since(t0) / reps,
+           reps, issue_us);
   }
   if (reps > 0 && streams > 1) {
     // independent convolutions (a batch each) on `streams` contexts: the

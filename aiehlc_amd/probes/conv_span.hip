@@ -15,10 +15,16 @@
 //   staging / mfma / epilogue cycles per wave (median and max)
 //   clock_ghz          shader cycles per wall-clock ns, averaged over waves
 // and the time per back-to-back launch of both instantiations (HIP events).
+// For the product instantiation it also reports the host's time per launch
+// alone (host_issue_us) and the device's own time per launch with the queue
+// already filled (device_us): 1000 launches queued behind a one-wave kernel
+// that waits a fixed wall-clock time longer than the host needs to queue
+// them, bracketed by events after the wait and after the last launch.
 // Prints one JSON object.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -44,6 +50,15 @@ uint64_t mix(uint64_t z) {
   z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
   return z ^ (z >> 31);
 }
+
+// One wave that returns once `ticks` of the 100 MHz constant clock have
+// passed: a wait of fixed length that ends on its own.
+__global__ __launch_bounds__(64) void timed_wait(unsigned long long ticks) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(100);
+}
+
+using clk = std::chrono::steady_clock;
 
 double median(std::vector<double> v) {
   std::sort(v.begin(), v.end());
@@ -83,15 +98,34 @@ int main(int argc, char** argv) {
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
+  double issue_us = 0;  // host time per launch of the last per_launch_us loop
   auto per_launch_us = [&](auto fn) {
     for (int i = 0; i < 500; ++i) fn();
     CHECK(hipEventRecord(e0, st));
+    const auto t0 = clk::now();
     for (int i = 0; i < launches; ++i) fn();
+    issue_us = std::chrono::duration<double, std::micro>(clk::now() - t0).count() / launches;
     CHECK(hipEventRecord(e1, st));
     CHECK(hipEventSynchronize(e1));
     float ms = 0;
     CHECK(hipEventElapsedTime(&ms, e0, e1));
     return ms * 1e3 / launches;
+  };
+  // the device's own time per launch: nq launches queued behind a wait of
+  // (host issue + 2) us per launch, at most 40 ms
+  bool outlasted = false;
+  auto device_us = [&](auto fn, double host_us) {
+    const int nq = 1000;
+    const double wait_us = nq * (host_us + 2.0) < 40000.0 ? nq * (host_us + 2.0) : 40000.0;
+    hipLaunchKernelGGL(timed_wait, dim3(1), dim3(64), 0, st, (unsigned long long)(wait_us * 100.0));
+    CHECK(hipEventRecord(e0, st));
+    for (int i = 0; i < nq; ++i) fn();
+    outlasted = hipEventQuery(e0) == hipErrorNotReady;
+    CHECK(hipEventRecord(e1, st));
+    CHECK(hipEventSynchronize(e1));
+    float ms = 0;
+    CHECK(hipEventElapsedTime(&ms, e0, e1));
+    return ms * 1e3 / nq;
   };
 
   product();
@@ -100,6 +134,8 @@ int main(int argc, char** argv) {
   std::vector<int8_t> y0(yb), y1(yb);
   CHECK(hipMemcpy(y0.data(), Y, yb, hipMemcpyDeviceToHost));
   const double us_product = per_launch_us(product);
+  const double issue_product = issue_us;
+  const double dev_product = device_us(product, issue_product);
   const double us_timed = per_launch_us(timed);  // its last launch leaves the probe words
   CHECK(hipGetLastError());
   CHECK(hipStreamSynchronize(st));
@@ -126,10 +162,12 @@ int main(int argc, char** argv) {
          "\"timed_output_equals_product\": %s, \"span_us\": %.3f, \"last_start_us\": %.3f, "
          "\"staging_cycles\": [%.0f, %.0f], \"mfma_cycles\": [%.0f, %.0f], \"epilogue_cycles\": [%.0f, %.0f], "
          "\"clock_ghz\": %.3f, \"us_per_launch_product\": %.3f, \"us_per_launch_timed\": %.3f, \"launches\": %d, "
+         "\"host_issue_us\": %.3f, \"device_us\": %.3f, \"blocker_outlasted_issue\": %s, "
          "\"cycles_are\": \"[median, max] over the %d waves of the last launch\"}\n",
          same ? "true" : "false", span_us, (double)(last0 - wall0) / 100.0, median(stg),
          *std::max_element(stg.begin(), stg.end()), median(mf), *std::max_element(mf.begin(), mf.end()),
-         median(ep), *std::max_element(ep.begin(), ep.end()), ghz, us_product, us_timed, launches, waves);
+         median(ep), *std::max_element(ep.begin(), ep.end()), ghz, us_product, us_timed, launches, issue_product,
+         dev_product, outlasted ? "true" : "false", waves);
   CHECK(hipFree(X));
   CHECK(hipFree(W));
   CHECK(hipFree(Y));

@@ -1,14 +1,23 @@
-// launch_floor — the time per launch of a kernel that does nothing, issued
-// back to back on one stream, for the grid shapes and LDS sizes of the
-// library's kernels.  A launch of a real kernel cannot take less than this on
-// the same GPU: the command processor's dispatch, the workgroup launch (the
-// LDS allocation included) and the end-of-kernel completion are all in it.
-// The int8 conv of the benchmark (8x56x56x64, 3x3) is a few microseconds of
-// work, so its time per launch is read against this floor.
+// launch_floor — what a launch costs apart from its kernel's work, for the
+// grid shapes and LDS sizes of the library's kernels, with an empty kernel
+// issued back to back on one stream.  Three figures per grid:
+//   us_per_launch       host loop of launches, then a drain: the rate one
+//                       host thread gets (events around the loop)
+//   host_issue_us       the host's time in hipLaunchKernel per launch (the
+//                       loop alone, before the drain)
+//   device_us           the device's own rate: the launches are queued behind
+//                       a one-wave kernel that waits a fixed wall-clock time
+//                       (longer than the host needs to queue them), and
+//                       events after the wait and after the last launch
+//                       bracket them; blocker_outlasted_issue says whether the
+//                       whole batch was queued before the wait ended
+// When host_issue_us exceeds device_us, a host thread issuing one launch
+// after another is what limits the back-to-back rate, not the device.
 //
-// Prints one JSON object: per grid shape, microseconds per back-to-back launch.
+// Prints one JSON object.
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 
@@ -27,6 +36,13 @@ __global__ __launch_bounds__(THREADS) void empty_kernel(int* out, int magic) {
   }
 }
 
+// One wave that returns once `ticks` of the 100 MHz constant clock have
+// passed: a wait of fixed length that ends on its own.
+__global__ __launch_bounds__(64) void timed_wait(unsigned long long ticks) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(100);
+}
+
 #define CHECK(x)                                                        \
   do {                                                                  \
     hipError_t e_ = (x);                                                \
@@ -36,23 +52,50 @@ __global__ __launch_bounds__(THREADS) void empty_kernel(int* out, int magic) {
     }                                                                   \
   } while (0)
 
+using clk = std::chrono::steady_clock;
+static double us_since(clk::time_point t) { return std::chrono::duration<double, std::micro>(clk::now() - t).count(); }
+
 template <int LDS_BYTES, int THREADS>
-void run(int* out, int blocks, int iters, const char* name, bool last) {
-  auto launch = [&]() { hipLaunchKernelGGL((empty_kernel<LDS_BYTES, THREADS>), dim3(blocks), dim3(THREADS), 0, 0, out, 0); };
+void run(hipStream_t st, int* out, int blocks, int iters, const char* name, bool last) {
+  auto launch = [&]() {
+    hipLaunchKernelGGL((empty_kernel<LDS_BYTES, THREADS>), dim3(blocks), dim3(THREADS), 0, st, out, 0);
+  };
   for (int i = 0; i < 2000; ++i) launch();
   CHECK(hipGetLastError());
-  CHECK(hipDeviceSynchronize());
+  CHECK(hipStreamSynchronize(st));
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
-  CHECK(hipEventRecord(e0));
+
+  // host loop, then drain
+  CHECK(hipEventRecord(e0, st));
+  const auto t0 = clk::now();
   for (int i = 0; i < iters; ++i) launch();
-  CHECK(hipEventRecord(e1));
+  const double issue_us = us_since(t0) / iters;
+  CHECK(hipEventRecord(e1, st));
   CHECK(hipEventSynchronize(e1));
   float ms = 0;
   CHECK(hipEventElapsedTime(&ms, e0, e1));
-  printf("  \"%s\": {\"workgroups\": %d, \"threads\": %d, \"lds_bytes\": %d, \"us_per_launch\": %.3f}%s\n", name, blocks,
-         THREADS, LDS_BYTES, ms * 1e3 / iters, last ? "" : ",");
+  const double loop_us = ms * 1e3 / iters;
+
+  // queued behind a wait of 4 us per launch (2 us more than the host's
+  // issue time measured above, at most 40 ms)
+  const int nq = 1000;
+  const double wait_us = nq * (issue_us + 2.0) < 40000.0 ? nq * (issue_us + 2.0) : 40000.0;
+  hipLaunchKernelGGL(timed_wait, dim3(1), dim3(64), 0, st, (unsigned long long)(wait_us * 100.0));
+  CHECK(hipEventRecord(e0, st));
+  for (int i = 0; i < nq; ++i) launch();
+  const bool outlasted = hipEventQuery(e0) == hipErrorNotReady;
+  CHECK(hipEventRecord(e1, st));
+  CHECK(hipEventSynchronize(e1));
+  CHECK(hipGetLastError());
+  CHECK(hipEventElapsedTime(&ms, e0, e1));
+  const double device_us = ms * 1e3 / nq;
+
+  printf("  \"%s\": {\"workgroups\": %d, \"threads\": %d, \"lds_bytes\": %d, \"us_per_launch\": %.3f, "
+         "\"host_issue_us\": %.3f, \"device_us\": %.3f, \"blocker_outlasted_issue\": %s}%s\n",
+         name, blocks, THREADS, LDS_BYTES, loop_us, issue_us, device_us, outlasted ? "true" : "false",
+         last ? "" : ",");
   CHECK(hipEventDestroy(e0));
   CHECK(hipEventDestroy(e1));
 }
@@ -60,14 +103,17 @@ void run(int* out, int blocks, int iters, const char* name, bool last) {
 int main(int argc, char** argv) {
   const int iters = argc > 1 ? atoi(argv[1]) : 5000;
   int* out = nullptr;
+  hipStream_t st;
+  CHECK(hipStreamCreate(&st));
   CHECK(hipMalloc(&out, 4096 * sizeof(int)));
   printf("{\n");
   // conv2d_i8_rows<3,3,64,2,64> at N=8, 56x56: 224 workgroups (8 x 28 x 1) of 512 threads, 65024 B of LDS
-  run<65024, 512>(out, 224, iters, "conv2d_rows_grid", false);
+  run<65024, 512>(st, out, 224, iters, "conv2d_rows_grid", false);
   // gemm_i8_pipe16<256,256> at 4096^3: 256 workgroups of 256 threads, 160 KiB of LDS
-  run<163840, 256>(out, 256, iters, "gemm_256x256_grid", false);
-  run<0, 64>(out, 1, iters, "one_wave", true);
+  run<163840, 256>(st, out, 256, iters, "gemm_256x256_grid", false);
+  run<0, 64>(st, out, 1, iters, "one_wave", true);
   printf("}\n");
   CHECK(hipFree(out));
+  CHECK(hipStreamDestroy(st));
   return 0;
 }

@@ -18,10 +18,13 @@ Also in the line (not the headline):
   extras.gemm_in_kernel  the headline kernel's in-kernel clocks (prologue,
                          cycles per k-tile, epilogue, workgroup end spread,
                          clock per XCD; aiehlc_amd/probes/gemm_span)
-  extras.launch_floor    time per back-to-back launch of an empty kernel with the
-                         conv's and the GEMM's grid and LDS size
-                         (aiehlc_amd/probes/launch_floor); the conv line carries
-                         its own floor and the time above it
+  extras.launch_floor    an empty kernel with the conv's and the GEMM's grid and
+                         LDS size (aiehlc_amd/probes/launch_floor): time per
+                         back-to-back launch from one host thread, the host's
+                         issue time per launch, and the device's time per
+                         launch with the queue already filled; the conv line
+                         carries the device figure as its floor and the time
+                         above it
   extras.reference_flow_16x16, extras.reference_flow_8x8
                          the reference's own timed example flow (aieml_mm.cc:
                          an int32 tile moved in, run, waited for, moved out)
@@ -259,10 +262,11 @@ def probe_json(exe: str) -> dict | None:
     return json.loads(r.stdout)
 
 
-def cpp_conv_loop(reps: int, streams: int = 1) -> float | None:
-    """us per call of the config-4 conv from the C++ harness: back to back on
-    one stream, or (streams > 1) independent calls dealt round-robin over that
-    many streams, each stream's output checked against the first's."""
+def cpp_conv_loop(reps: int, streams: int = 1) -> tuple[float, float | None] | None:
+    """(us per call, host issue us per call or None) of the config-4 conv from
+    the C++ harness: back to back on one stream, or (streams > 1) independent
+    calls dealt round-robin over that many streams, each stream's output
+    checked against the first's."""
     exe = os.path.join(ROOT, "aiehlc_amd", "harness", "miaie_examples")
     if not os.path.exists(exe):
         return None
@@ -271,7 +275,8 @@ def cpp_conv_loop(reps: int, streams: int = 1) -> float | None:
     m = re.search(pat, r.stdout)
     if r.returncode != 0 or not m:
         return None
-    return float(m.group(1))
+    mi = re.search(r"back-to-back: [0-9.]+ us per call over \d+ calls \(host issue ([0-9.]+) us per call\)", r.stdout)
+    return float(m.group(1)), (float(mi.group(1)) if mi and streams == 1 else None)
 
 
 def mfma_ceiling() -> dict | None:
@@ -390,15 +395,20 @@ def extra_conv(ctx, timer, args) -> dict:
     # the kernel's own execution time from in-kernel clocks (the same kernel
     # template, instantiated with clock records, in its own process)
     span = probe_json(CONV_SPAN_EXE)
+    issue_c = None
     if cpp is not None:
-        us_c, step_from = cpp, ("C++ harness, 3000 back-to-back miaie_conv2d_i8_nhwc calls "
-                                "(aiehlc_amd/harness/miaie_examples conv 3000)")
+        (us_c, issue_c), step_from = cpp, ("C++ harness, 3000 back-to-back miaie_conv2d_i8_nhwc calls "
+                                           "(aiehlc_amd/harness/miaie_examples conv 3000)")
     else:
         us_c, step_from = ms_c * 1e3, "Python loop over the ctypes binding, HIP events"
+    if cpp2 is not None:
+        cpp2 = cpp2[0]
     if isinstance(span, dict) and "span_us" in span:
         s_us = span["span_us"]
         span["alg_GBps"] = round(conv_bytes / (s_us * 1e-6) / 1e9, 1)
         span["frac"] = round(conv_ops / (s_us * 1e-6) / 1e12 / roof, 4)
+        if span.get("device_us"):
+            span["device_frac"] = round(conv_ops / (span["device_us"] * 1e-6) / 1e12 / roof, 4)
     return {
         "config": "N=8 H=W=56 Cin=Cout=64 3x3 stride 1 pad 1, NHWC x OHWI, per-channel shift in [8,12]",
         "kernel": "conv2d_i8_rows<3,3,64,2,64> (2 output rows x 64 channels per workgroup, image-per-XCD grid)",
@@ -410,6 +420,7 @@ def extra_conv(ctx, timer, args) -> dict:
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "alg_bytes": conv_bytes,
                      "roof_tops": round(roof, 1),
                      "frac": round(conv_ops / (us_c * 1e-6) / 1e12 / roof, 4)},
+        "host_issue_us_per_call": issue_c,
         "python_loop_us_per_step": round(ms_c * 1e3, 3),
         "two_streams": None if cpp2 is None else {
             "us_per_conv": round(cpp2, 3), "gops": round(conv_ops / (cpp2 * 1e-6) / 1e9, 1),
@@ -424,10 +435,12 @@ def extra_conv(ctx, timer, args) -> dict:
                              "how": "median of 50 launches, each alone between two events on a drained stream; "
                                     "cold_hbm writes 512 MiB before each launch (outside the events)"},
         "in_kernel": span,
-        "note": "events bracket back-to-back launches, so us_per_step includes the command processor's work "
-                "between launches (an empty kernel of the same grid: extras.launch_floor); in_kernel.span_us is "
-                "the first wave's start to the last wave's end by the GPU's wall clock "
-                "(aiehlc_amd/probes/conv_span); graph_chain replays 20 recorded convolutions per launch",
+        "note": "us_per_step is the host's clock around back-to-back calls and the drain after them, so it "
+                "includes the device's work between launches (an empty kernel of the same grid: "
+                "extras.launch_floor.conv2d_rows_grid.device_us) and would show a host slower than the device "
+                "(host_issue_us_per_call); in_kernel.device_us is the same kernel's time per launch with the queue "
+                "already filled, in_kernel.span_us the first wave's start to the last wave's end by the GPU's wall "
+                "clock (aiehlc_amd/probes/conv_span); graph_chain replays 20 recorded convolutions per launch",
     }
 
 
@@ -644,10 +657,13 @@ def main() -> int:
         extras["launch_floor"] = floor
         conv = extras.get("conv2d_3x3")
         cf = (floor or {}).get("conv2d_rows_grid")
-        if conv and isinstance(cf, dict):
-            # the same grid and LDS with an empty kernel body, in its own process
-            conv["launch_floor_us"] = cf["us_per_launch"]
-            conv["us_above_floor"] = round(conv["us_per_step"] - cf["us_per_launch"], 3)
+        if conv and isinstance(cf, dict) and "device_us" in cf:
+            # the same grid and LDS with an empty kernel body, in its own
+            # process: the device's time per launch with the queue filled,
+            # and the host's time to issue one launch
+            conv["launch_floor_us"] = cf["device_us"]
+            conv["launch_host_issue_us"] = cf["host_issue_us"]
+            conv["us_above_floor"] = round(conv["us_per_step"] - cf["device_us"], 3)
         extras["vendor_library"] = vendor_library(args.steps)
 
     roofline = {
