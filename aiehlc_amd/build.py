@@ -146,7 +146,7 @@ def build_harness(verbose: bool = False) -> None:
         if f.endswith(".cpp"):
             exe = os.path.join(HARNESS, f[:-4])
             cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", f"-I{os.path.join(ROOT, 'include')}",
-                   os.path.join(HARNESS, f), "-o", exe + ".tmp", f"-L{LIBDIR}", "-lmiaie",
+                   os.path.join(HARNESS, f), "-o", exe + ".tmp", f"-L{LIBDIR}", "-lmiaie", "-pthread",
                    "-Wl,-rpath,$ORIGIN/../lib"]
         elif f.endswith(".c"):
             # C programs written against the aie-rt-shaped facade
