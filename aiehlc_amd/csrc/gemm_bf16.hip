@@ -293,7 +293,8 @@ static_assert(PAIR_LDS <= 163840, "pair-staged LDS budget");
 // at 1.60 GHz on the 32x32x16 form, same GPU, same run).  The k-loop follows
 // the int8 kernel gemm_i8_pipe16 (gemm_i8_kernels.hpp): each wave's 128x128
 // quarter is 8 x 8 blocks of 16 x 16, a 32-wide k-tile is one k-step, block
-// rows 0-3 are multiplied in phase 1 and 4-7 in phase 2 (column-block-major),
+// rows 0-3 are multiplied in phase 1 and 4-7 in phase 2 (column-block-major,
+// rows reversed on odd column blocks so consecutive MFMAs share an operand),
 // one set of fragment registers, accumulators updated in place by inline
 // MFMAs (the int8 kernel's notes on why, and the CPU check of the generated
 // assembly, apply here too).
@@ -466,7 +467,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair16(const uint16_t* __res
     constexpr int qa1 = PAR == 0 ? 1 : 3;
 #pragma unroll
     for (int x = 0; x < PH; ++x) {
-      const int j = x / HI, i = x % HI;
+      const int j = x / HI, i = dev::snake_j<HI>(x);
       mfma16_bf16(acc[i][j], bfrag(j), alo[i]);
       if (x < HI) ahi[x] = read_a(sa0, PAR, HI + x);
 #pragma unroll
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair16(const uint16_t* __res
     const uint32_t sa_next = PAR == 0 ? sa0 : sa1;
 #pragma unroll
     for (int x = 0; x < PH; ++x) {
-      const int j = x / HI, i = x % HI;
+      const int j = x / HI, i = dev::snake_j<HI>(x);
       mfma16_bf16(acc[HI + i][j], bfrag(j), ahi[i]);
 #pragma unroll
       for (int c = 0; c < NB2 + NA2_; ++c)
@@ -499,7 +500,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair16(const uint16_t* __res
         }
       if constexpr (NEXT) {
         if (x < HI) alo[x] = read_a(sa_next, 1 - PAR, x);
-        if (i == HI - 1) read_b(sb1, j);  // after the last use of tile t's B fragment j
+        if (x % HI == HI - 1) read_b(sb1, j);  // after the last use of tile t's B fragment j
       }
       dev::sched_fence();
     }

@@ -530,7 +530,9 @@ constexpr int PROBE_WORDS = 6;
 // A wave's WM x WN quarter is NI x NJ blocks of 16 x 16 (NI = WM/16, NJ =
 // WN/16), and one 64-wide k-tile is one k-step.  Block (i, j) of k-tile t is
 // multiplied in phase 1 of tile t for i < NI/2 and in phase 2 for i >= NI/2,
-// column-block-major (j outer, i inner) in both phases:
+// column-block-major (j outer, i inner, i reversed on odd j, so consecutive
+// MFMAs always share an operand: 1.2% faster at 4096^3 under the power
+// limit than restarting i at every column block) in both phases:
 //   phase 1: A fragments 0 .. NI/2-1 (alo) and the B fragments, while A
 //            fragments NI/2 .. NI-1 of tile t (ahi) are read;
 //   barrier (tile t+1 landed);
@@ -766,7 +768,7 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int m0, int n0, const i
     constexpr int qa1 = PAR == 0 ? 1 : 3;
 #pragma unroll
     for (int x = 0; x < PH; ++x) {
-      const int j = x / HI, i = x % HI;
+      const int j = x / HI, i = dev::snake_j<HI>(x);
       mfma16(acc[i][j], bfrag(j), alo[i]);
       if (x < HI) ahi[x] = read_a(sa0, PAR, HI + x);
 #pragma unroll
@@ -790,7 +792,7 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int m0, int n0, const i
     const uint32_t sa_next = PAR == 0 ? sa0 : sa1;  // pair of tile t+1
 #pragma unroll
     for (int x = 0; x < PH; ++x) {
-      const int j = x / HI, i = x % HI;
+      const int j = x / HI, i = dev::snake_j<HI>(x);
       mfma16(acc[HI + i][j], bfrag(j), ahi[i]);
 #pragma unroll
       for (int c = 0; c < NB2 + NA2_; ++c)
@@ -802,7 +804,7 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int m0, int n0, const i
         }
       if constexpr (NEXT) {
         if (x < HI) alo[x] = read_a(sa_next, 1 - PAR, x);
-        if (i == HI - 1) {  // last use of tile t's B fragment j
+        if (x % HI == HI - 1) {  // last use of tile t's B fragment j
 #pragma unroll
           for (int r = 0; r < BPF; ++r) read_b(sb1, j, r);
         }
