@@ -22,6 +22,7 @@ CASES = [
     (["gemm", "512", "384", "192", "9"], "CPU result matches"),
     (["conv"], "CPU result matches"),
     (["conv", "200", "2"], "CPU result matches"),  # also two streams, each output against the first
+    (["conv", "300", "3"], "from 3 threads"),  # three streams, one issuing thread each, outputs compared
     (["mlp", "256", "4096", "11008", "4096"], "CPU result matches"),
 ]
 
@@ -41,5 +42,7 @@ def test_harness_example(args, needle):
     print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
     assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
     assert needle in r.stdout
+    if args[0] == "conv":
+        assert "CPU result matches" in r.stdout
     if args[:4] == ["gemm", "4096", "4096", "4096"]:  # the planner, read through miaie::Context
         assert "plan: kernel 1, tile 256x256, 256 workgroups of 256 threads" in r.stdout
