@@ -370,3 +370,46 @@ def test_random_shapes_match_the_oracle(ctx, M, N, K, layout, shift, relu, cus):
     assert np.array_equal(C2, Co)
     assert np.array_equal(Y, Yo)
     assert np.array_equal(Y2, Yo)
+
+
+# The pipelined kernels start the accumulators of a Y-only launch at the
+# rounding term 2^(s-1), exact while |acc| + 2^(s-1) < 2^31, which the
+# launcher holds to K < 2^16 (|acc| <= K * 2^14); K = 65472 is the largest
+# such K the pipelined kernels take, where an all -128 row times an all -128
+# column gives acc = 2^30 - 2^20 and, at s = 31, acc + 2^30 lies 2^20 below
+# 2^31.  K = 65536 takes the 64x64 kernel, whose requant rounds without the
+# add ((acc >> s) + bit s-1 of acc).  Rows 0-2 of A and columns 0-2 of B are
+# constant (-128, -128, 127) so that the top-left 3x3 block of accumulators
+# sits at the extremes +-K*2^14; the rest is random.
+@pytest.mark.parametrize("K,MN", [(65472, 256), (65536, 128)])
+@pytest.mark.parametrize("layout", [mi.B_NN, mi.B_NT])
+def test_requant_round_term_at_the_largest_k(ctx, K, MN, layout):
+    M = N = MN
+    plan = ctx.plan_gemm_i8(M, N, K)
+    print(f"[case] requant boundary gemm {M}x{N}x{K} layout {layout} plan {plan}", flush=True)
+    assert (plan["kernel"] == mi.KERNEL_TILE64) == (K >= 1 << 16)
+    rng = np.random.default_rng(K + MN + layout)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    Bkn = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    for r, v in enumerate((-128, -128, 127)):
+        A[r, :] = v
+        Bkn[:, r] = v
+    B = np.ascontiguousarray(Bkn.T) if layout == mi.B_NT else Bkn
+    Co = oracle.gemm_i8(A, B, b_nt=layout == mi.B_NT)
+    assert Co[0, 0] == K * 16384 and Co[0, 2] == -K * 16256
+    dA, dB = ctx.upload(A), ctx.upload(B)
+    dY, dY2, dC2 = ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int8), ctx.empty((M, N), np.int32)
+    try:
+        for shift in (0, 1, 16, 29, 30, 31):
+            for relu in (False, True):
+                ctx.gemm_i8_rq(dA, dB, dY, M, N, K, shift, relu, None, layout)
+                ctx.gemm_i8_rq(dA, dB, dY2, M, N, K, shift, relu, dC2, layout)
+                ctx.wait(60_000)
+                Yo = oracle.requant(Co, shift, relu=relu)
+                Y, Y2, C2 = ctx.download(dY), ctx.download(dY2), ctx.download(dC2)
+                assert np.array_equal(Y, Yo), (shift, relu, int(np.count_nonzero(Y != Yo)))
+                assert np.array_equal(Y2, Yo), (shift, relu)
+                assert np.array_equal(C2, Co), (shift, relu)
+    finally:
+        for b in (dA, dB, dY, dY2, dC2):
+            b.free()
