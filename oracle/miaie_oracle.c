@@ -255,12 +255,15 @@ ORACLE_API void oracle_gemm_bf16_f64_rows(const uint16_t* A, const uint16_t* B, 
 #pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
 #endif
   for (int i = row0; i < row1; ++i) {
+    double* arow = (double*)malloc((size_t)K * sizeof(double) + 8);
+    for (int k = 0; k < K; ++k) arow[k] = oracle_bf16_to_f32(A[(size_t)i * K + k]);
     for (int j = 0; j < N; ++j) {
       double acc = 0.0;
       const double* b = Bt + (size_t)j * K;
-      for (int k = 0; k < K; ++k) acc += (double)oracle_bf16_to_f32(A[(size_t)i * K + k]) * b[k];
+      for (int k = 0; k < K; ++k) acc += arow[k] * b[k];
       C[(size_t)(i - row0) * N + j] = acc;
     }
+    free(arow);
   }
   free(Bt);
   (void)nthreads;

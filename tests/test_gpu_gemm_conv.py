@@ -4,8 +4,8 @@ chained int8 MLP, through the miaie C ABI, against the CPU oracle.
 Integer paths are compared bit-exactly.  bf16 uses the normwise metric
 max|C - R| / max|R| <= 1e-2 against the fp64 oracle on the same bf16 inputs.
 The integer benchmark shapes (configs 1, 2, 4 and 5) are compared with the
-oracle over every element; bf16 8192^3 on row slabs plus a property that holds
-over the whole output.
+oracle over every element; bf16 8192^3 on one row of every 16-row block (every
+workgroup's output) plus checks that hold over the whole output.
 """
 import numpy as np
 import pytest
@@ -238,22 +238,35 @@ def test_gemm_bf16_k_sweep(ctx, K):
 
 
 def test_gemm_bf16_8192_config(ctx):
-    """Config 3: 8192^3 bf16, N(0,1)/sqrt(K).  On a 32-row slab and 32
-    scattered rows against the fp64 oracle: the normwise error (the bar,
-    max|C-R| / max|R| <= 1e-2), the elementwise relative error where
-    |R| >= 1e-3 max|R|, and the Frobenius relative error.  Over the whole
-    output: C(2A) == 2 C(A) bit for bit (doubling a bf16 operand is exact
-    and the accumulation order does not depend on the data)."""
+    """Config 3: 8192^3 bf16, N(0,1)/sqrt(K).
+
+    The output buffer is filled with NaN before the launch, so an element the
+    kernel never writes fails the finiteness check over the whole output.
+
+    Against the fp64 oracle on 512 rows, one from every 16-row block (row
+    16b + b mod 16): every 256-row tile row, every wave's half of it and
+    every 16-row MFMA block of a wave is compared on all 8192 columns, so
+    every one of the 1024 workgroups' output is checked.  Reported: the
+    normwise error (the bar, max|C-R| / max|R| <= 1e-2), the elementwise
+    relative error where |R| >= 1e-3 max|R|, and the Frobenius relative
+    error (also held to 1e-2).
+
+    Over the whole output: C(2A) == 2 C(A) bit for bit (doubling a bf16
+    operand is exact and the accumulation order does not depend on the
+    data)."""
     M = N = K = 8192
     _say("gemm_bf16 8192^3")
     A = synth.bf16_normal((M, K), 1, 1.0 / np.sqrt(K))
     B = synth.bf16_normal((K, N), 2, 1.0 / np.sqrt(K))
     A2 = synth.f32_to_bf16_bits(2.0 * synth.bf16_bits_to_f32(A))
     assert np.array_equal(synth.bf16_bits_to_f32(A2), 2.0 * synth.bf16_bits_to_f32(A))
-    dA, dB, dC = ctx.upload(A), ctx.upload(B), ctx.empty((M, N), np.float32)
+    nan_fill = np.full((M, N), np.nan, dtype=np.float32)
+    dA, dB, dC = ctx.upload(A), ctx.upload(B), ctx.upload(nan_fill)
     ctx.gemm_bf16_f32(dA, dB, dC, M, N, K)
     ctx.wait(120_000)
     Cg = ctx.download(dC)
+    ctx.copy_h2d(dC, nan_fill)
+    del nan_fill
     ctx.copy_h2d(dA, A2)
     ctx.gemm_bf16_f32(dA, dB, dC, M, N, K)
     ctx.wait(120_000)
@@ -263,7 +276,9 @@ def test_gemm_bf16_8192_config(ctx):
     assert np.isfinite(Cg).all()
     assert np.array_equal(C2, 2.0 * Cg)
     del C2
-    rows = np.concatenate([np.arange(32), np.random.default_rng(1).choice(np.arange(32, M), 32, replace=False)])
+    blocks = np.arange(M // 16)
+    rows = 16 * blocks + blocks % 16
+    assert np.array_equal(np.unique(rows // 16), blocks)
     R = oracle.gemm_bf16(A[rows], B, f64=True)
     D = Cg[rows].astype(np.float64) - R
     err = np.abs(D).max() / np.abs(R).max()
@@ -396,7 +411,8 @@ def test_conv2d_i8_taps_128_tiles(ctx, shape):
 
 @pytest.mark.parametrize("shape,cus", [
     ((1, 8, 8, 256, 128, 3, 3, 1, 1), 256),   # 32 x 32 waves (more workgroups), 64-column blocks
-    ((1, 8, 8, 256, 128, 3, 3, 1, 1), 1),     # 32 x 64 waves (two MFMAs per pixel fragment), 32-column blocks
+    ((1, 8, 8, 192, 128, 3, 3, 1, 1), 1),     # 32 x 64 waves (two MFMAs per pixel fragment), 32-column blocks
+    #                                           (Cin 192: at 1 CU the taps kernel would be estimated faster for Cin 256)
     ((2, 6, 70, 192, 128, 3, 3, 1, 0), 1),    # 3 chunks, two 64-column blocks, no padding, 32 x 64 waves
     ((16, 5, 9, 320, 128, 3, 3, 1, 1), 1),    # 5 chunks, image-per-XCD grid over 16 images, 32 x 64 waves
     ((2, 9, 20, 192, 128, 3, 3, 1, 1), 1),    # 8 rows x 32 columns, 32 x 64 waves, last row block partial
