@@ -9,6 +9,13 @@
 // address: miaie_init resolves the address on each device once
 // (scratch_setup, hipGetSymbolAddress) and kernels only ever see that
 // address.  Nothing here calls hipMalloc, hipFree or hipMemset*.
+//
+// Calls from different streams (contexts) on one GPU are ordered through one
+// event per device, created by the same set-up: under a host mutex each call
+// makes its stream wait for the event, queues its two GEMMs and records the
+// event after them, so the next call's first GEMM starts only after this
+// call's second GEMM has read H.  A call recorded into a graph takes no part
+// in that chain (its replays are not ordered against other calls).
 #include <mutex>
 
 #include "miaie_internal.hpp"
@@ -23,7 +30,8 @@ __device__ __align__(256) int8_t scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+void* g_scratch_ptr[kMaxDevices];       // device address of `scratch`, per device
+hipEvent_t g_scratch_ev[kMaxDevices];   // the last queued use of that array, per device
 
 }  // namespace
 
@@ -39,7 +47,11 @@ int scratch_setup(miaie_ctx* ctx) {
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress(scratch)");
     if (p == nullptr) return fail(ctx, MIAIE_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+    hipEvent_t ev = nullptr;
+    const hipError_t e2 = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e2 != hipSuccess) return hip_fail(ctx, e2, "hipEventCreateWithFlags(scratch order)");
     g_scratch_ptr[dev] = p;
+    g_scratch_ev[dev] = ev;
   }
   ctx->scratch = g_scratch_ptr[dev];
   return MIAIE_OK;
@@ -59,5 +71,17 @@ extern "C" int miaie_mlp_i8_noalloc(miaie_ctx* ctx, const int8_t* X, const int8_
                 "(MIAIE_MLP_NOALLOC_MAX_H); use miaie_mlp_i8 with a caller-provided H",
                 __func__, (size_t)M * (size_t)F, kScratchBytes);
   if (ctx->scratch == nullptr) return fail(ctx, MIAIE_EHIP, "%s: scratch address not resolved", __func__);
-  return mlp_i8_checked(ctx, __func__, X, W1, W2, static_cast<int8_t*>(ctx->scratch), Y, M, K, F, Nout, s1, s2);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  const hipEvent_t ev = g_scratch_ev[ctx->device];
+  if (!ctx->recording) {
+    const hipError_t e = hipStreamWaitEvent(ctx->stream, ev, 0);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamWaitEvent(scratch order)");
+  }
+  rc = mlp_i8_checked(ctx, __func__, X, W1, W2, static_cast<int8_t*>(ctx->scratch), Y, M, K, F, Nout, s1, s2);
+  if (!ctx->recording) {
+    // also after a failure: whatever part of the call was queued is ordered
+    const hipError_t e = hipEventRecord(ev, ctx->stream);
+    if (e != hipSuccess && rc == MIAIE_OK) return hip_fail(ctx, e, "hipEventRecord(scratch order)");
+  }
+  return rc;
 }

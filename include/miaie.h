@@ -129,7 +129,9 @@ MIAIE_API int miaie_plan_set_cus(miaie_ctx* ctx, int cus, int* previous);
  * reference's conv exists only as AIE graph configuration
  * (thirdparty/adf/aie_control.cpp:2554-2559), so there is no reference
  * counterpart; the choice is exposed so callers and tests can see it.  Needs
- * no context and no device.
+ * no context and no device: it reports the choice for a 256-CU MI355X.  A
+ * launch weighs the same estimates on its context's CU count (the device's,
+ * or miaie_plan_set_cus), which may pick another kernel where two apply.
  * Invalid shapes return MIAIE_EINVAL, as the entry point does. */
 #define MIAIE_CONV_ROWS 0   /* row-block kernel: 3x3, stride 1, Cin 32/64/128, Cout % 32 == 0 (rows in blocks of 64) */
 #define MIAIE_CONV_IGEMM 1  /* implicit-GEMM kernel: Cin % 32 == 0, Cout % 64 == 0 */
@@ -259,9 +261,12 @@ MIAIE_API int miaie_mlp_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W1, co
  * device array of MIAIE_MLP_NOALLOC_MAX_H bytes that every GPU the library
  * runs on holds from miaie_init until the process ends.  M*F above that
  * returns MIAIE_EINVAL without launching.  The call allocates nothing.  All
- * calls on one GPU share that GPU's array: calls that overlap on one GPU
- * (from two streams or contexts) race on it; calls queued on one stream do
- * not. */
+ * calls on one GPU share that GPU's array.  Eager calls from different
+ * streams or contexts are ordered on the device (each waits for the previous
+ * call's use of the array through one event per GPU), so they queue behind
+ * each other rather than overlap.  A call recorded into a graph is not part
+ * of that order: its replays race with any other use of the array that
+ * overlaps them on the same GPU. */
 #define MIAIE_MLP_NOALLOC_MAX_H ((size_t)32 << 20)
 MIAIE_API int miaie_mlp_i8_noalloc(miaie_ctx* ctx, const int8_t* X, const int8_t* W1, const int8_t* W2, int8_t* Y,
                                    int M, int K, int F, int Nout, int s1, int s2);
