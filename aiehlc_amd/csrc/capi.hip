@@ -92,7 +92,7 @@ extern "C" int miaie_plan_conv2d_i8(int N, int H, int W_, int Cin, int Cout, int
   if (!kernel) return fail(nullptr, MIAIE_EINVAL, "%s: kernel is NULL", __func__);
   int rc = check_conv_shape(nullptr, __func__, N, H, W_, Cin, Cout, R, S, stride, pad);
   if (rc) return rc;
-  *kernel = conv2d_kernel_for(N, H, W_, Cin, Cout, R, S, stride, pad, true, true);
+  *kernel = conv2d_kernel_for(N, H, W_, Cin, Cout, R, S, stride, pad, true, true, 256);
   return MIAIE_OK;
 }
 

@@ -543,13 +543,11 @@ static double taps_us(size_t P, int Cin, int Cout, int R, int S, int cus, size_t
   return launch_rounds(t64 * ks, cus) * (2.5 + 0.41 * stages / ks) + (ks > 1 ? 3.0 : 0.0);
 }
 
-// The kernel choice is made for a 256-CU device (MI355X) whatever the
-// context's CU count, so miaie_plan_conv2d_i8 (no context) and every launch
-// agree; the tile choices within one kernel use the context's CU count.
-constexpr int CONV_PLAN_CUS = 256;
-
+// The kernel choice weighs estimated times on `cus` compute units: the
+// context's count at launch (miaie_plan_set_cus or the device's), and an
+// MI355X's 256 for miaie_plan_conv2d_i8, which has no context.
 int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad, bool aligned16,
-                      bool shifts_aligned4) {
+                      bool shifts_aligned4, int cus) {
   const int Ho = (H + 2 * pad - R) / stride + 1;
   const int Wo = (Wd + 2 * pad - S) / stride + 1;
   const size_t P = (size_t)N * Ho * Wo;
@@ -572,8 +570,8 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
     // fewer empty columns on narrow layers, which pays where the row-block
     // kernel's grid takes more than one round of CUs
     if (Cin == 128 && deep_ok) {
-      const RowsDeepTile t = rows_deep_tile(N, Ho, Wo, Cin, Cout, CONV_PLAN_CUS);
-      if (rows_deep_us(N, Ho, Wo, Cin, Cout, t, CONV_PLAN_CUS) < rows128_us(N, Ho, Wo, Cout, CONV_PLAN_CUS))
+      const RowsDeepTile t = rows_deep_tile(N, Ho, Wo, Cin, Cout, cus);
+      if (rows_deep_us(N, Ho, Wo, Cin, Cout, t, cus) < rows128_us(N, Ho, Wo, Cout, cus))
         return MIAIE_CONV_ROWS_DEEP;
     }
     return MIAIE_CONV_ROWS;
@@ -584,9 +582,9 @@ int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int
                        (size_t)N * H * Wd * Cin < ((size_t)1 << 31) && (size_t)Cout * R * S * Cin < ((size_t)1 << 31) &&
                        P < ((size_t)1 << 31) && Cout / 64 <= 65535;
   if (deep_ok && taps_ok) {
-    const RowsDeepTile t = rows_deep_tile(N, Ho, Wo, Cin, Cout, CONV_PLAN_CUS);
-    return rows_deep_us(N, Ho, Wo, Cin, Cout, t, CONV_PLAN_CUS) <=
-                   taps_us(P, Cin, Cout, R, S, CONV_PLAN_CUS, MIAIE_CTX_WORK_BYTES)
+    const RowsDeepTile t = rows_deep_tile(N, Ho, Wo, Cin, Cout, cus);
+    return rows_deep_us(N, Ho, Wo, Cin, Cout, t, cus) <=
+                   taps_us(P, Cin, Cout, R, S, cus, MIAIE_CTX_WORK_BYTES)
                ? MIAIE_CONV_ROWS_DEEP
                : MIAIE_CONV_TAPS;
   }
@@ -604,7 +602,8 @@ int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uin
   const int Wo = (Wd + 2 * pad - S) / stride + 1;
   const size_t P = (size_t)N * Ho * Wo;
   const int kernel = conv2d_kernel_for(N, H, Wd, Cin, Cout, R, S, stride, pad,
-                                       aligned(X, 16) && aligned(W, 16) && aligned(Y, 16), aligned(shifts, 4));
+                                       aligned(X, 16) && aligned(W, 16) && aligned(Y, 16), aligned(shifts, 4),
+                                       ctx->cus);
   if (kernel == MIAIE_CONV_ROWS) {
     if (Cin == 128) return launch_rows<128>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);
     if (Cin == 64) return launch_rows<64>(ctx, X, W, shifts, Y, N, H, Wd, Cout, pad, Ho, Wo);

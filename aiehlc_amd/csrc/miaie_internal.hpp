@@ -67,9 +67,10 @@ int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, 
 int plan_gemm_i8(miaie_ctx* ctx, int M, int N, int K, int dense_ok, miaie_gemm_plan* plan);
 int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float* C, int M, int N,
                      int K);
-// MIAIE_CONV_* kernel for a shape (conv2d_i8.hip); the shape must be valid.
+// MIAIE_CONV_* kernel for a shape on `cus` compute units (conv2d_i8.hip);
+// the shape must be valid.
 int conv2d_kernel_for(int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride, int pad, bool aligned16,
-                      bool shifts_aligned4);
+                      bool shifts_aligned4, int cus);
 int launch_conv2d_i8(miaie_ctx* ctx, const int8_t* X, const int8_t* W, const uint8_t* shifts,
                      int8_t* Y, int N, int H, int Wd, int Cin, int Cout, int R, int S, int stride,
                      int pad);

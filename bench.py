@@ -37,8 +37,10 @@ Also in the line (not the headline):
                          example/matrixmultiply/aieml_mm.cc:194-230), restated
                          in oracle/miaie_oracle.c, on this host's cores
 
-roofline.traffic is read from profiles/gemm_i8_rq_4096_traffic.txt, which
-records the rocprofv3 FETCH_SIZE / WRITE_SIZE runs it comes from.
+roofline.traffic (L2<->fabric bytes per launch, MALL hits included) and
+roofline.frac_rocprof are read from profiles/gemm_i8_rq_4096_traffic.txt, which
+records the rocprofv3 FETCH_SIZE / WRITE_SIZE and kernel-trace runs they come
+from.
 """
 from __future__ import annotations
 
@@ -139,13 +141,22 @@ def single_launch_us(ctx, timer, fn, reps: int, flush=None) -> float:
     return ts[len(ts) // 2]
 
 
-def read_traffic() -> tuple[int | None, str | None]:
-    """HBM bytes per launch recorded in the committed rocprofv3 summary."""
+def read_traffic() -> dict:
+    """The committed rocprofv3 summary of the headline kernel: L2<->fabric
+    bytes per launch (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size;
+    reads served by the MALL are counted in FETCH_SIZE too), the kernel-trace
+    average duration and the bench's own event time in that profiled run."""
+    out = {"bytes": None, "source": None, "rocprof_avg_kernel_us": None, "event_us": None}
     if not os.path.exists(TRAFFIC_FILE):
-        return None, None
+        return out
     text = open(TRAFFIC_FILE).read()
-    m = re.search(r"^hbm_bytes_per_launch:\s*(\d+)", text, re.M)
-    return (int(m.group(1)) if m else None), os.path.relpath(TRAFFIC_FILE, ROOT)
+    out["source"] = os.path.relpath(TRAFFIC_FILE, ROOT)
+    for key, pat, conv in (("bytes", r"^l2_fabric_bytes_per_launch:\s*(\d+)", int),
+                           ("rocprof_avg_kernel_us", r"^rocprof_avg_kernel_us:\s*([\d.]+)", float),
+                           ("event_us", r"^bench_event_us_same_run:\s*([\d.]+)", float)):
+        m = re.search(pat, text, re.M)
+        out[key] = conv(m.group(1)) if m else None
+    return out
 
 
 def cpu_baseline(seconds: float) -> dict:
@@ -645,7 +656,7 @@ def main() -> int:
     tops = ops / (ms * 1e-3) / 1e12
     for b in (dA, dB, dY):
         b.free()
-    traffic, traffic_src = read_traffic()
+    prof = read_traffic()
 
     extras = {}
     if not args.no_extras:
@@ -682,10 +693,19 @@ def main() -> int:
         "kernel": "gemm_i8_pipe16<256, 256, 4, NN, Y_HI> (rocprof: miaie::gemm::gemm_i8_pipe16<256, 256, 4, false, 2, false, false, false>)",
         "achieved": round(tops, 2),
         "peak": PEAK_INT8_TOPS,
-        "unit": "TFLOP/s",
+        "unit": "TOP/s",
         "frac": round(tops / PEAK_INT8_TOPS, 4),
-        "traffic": traffic,
-        "traffic_source": traffic_src,
+        # L2<->fabric bytes per launch (FETCH_SIZE + WRITE_SIZE; MALL hits
+        # are counted), from the committed profile
+        "traffic": prof["bytes"],
+        "traffic_source": prof["source"],
+        # the same fraction from the committed rocprofv3 kernel-trace average,
+        # and the bench's own event time per launch in that profiled run (the
+        # box differs from this one: boxes of the pool spread by about 10%)
+        "frac_rocprof": (round(ops / (prof["rocprof_avg_kernel_us"] * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4)
+                         if prof["rocprof_avg_kernel_us"] else None),
+        "rocprof_avg_kernel_us": prof["rocprof_avg_kernel_us"],
+        "profiled_run_event_us": prof["event_us"],
         "alg_ops_per_launch": ops,
         "alg_bytes_per_launch": M * K + K * N + M * N,
     }

@@ -67,7 +67,7 @@ def test_status_codes_match_header():
         assert m and int(m.group(1)) == getattr(mi, name), name
     # the conv planner's kernel ids, as the Python binding names them
     for name, label in (("MIAIE_CONV_ROWS", "rows"), ("MIAIE_CONV_IGEMM", "igemm"), ("MIAIE_CONV_DIRECT", "direct"),
-                        ("MIAIE_CONV_TAPS", "taps")):
+                        ("MIAIE_CONV_TAPS", "taps"), ("MIAIE_CONV_ROWS_DEEP", "rows_deep")):
         m = re.search(rf"#define {name} (\d+)", text)
         assert m and mi.CONV_KERNELS[int(m.group(1))] == label, name
 
