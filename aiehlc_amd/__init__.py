@@ -25,7 +25,8 @@ from . import synth  # noqa: F401  (re-exported)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 # MIAIE_LIB_DIR selects another build of the same library (the host-sanitized
-# one in aiehlc_amd/lib_san, see aiehlc_amd/build.py); default aiehlc_amd/lib
+# one in aiehlc_amd/lib_san, the device-checked one in aiehlc_amd/lib_dbg, see
+# aiehlc_amd/build.py); default aiehlc_amd/lib
 LIB_DIR = os.environ.get("MIAIE_LIB_DIR") or os.path.join(HERE, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmiaie.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "miaie.h")
@@ -36,6 +37,7 @@ MIAIE_EHIP = -2
 MIAIE_ETIMEDOUT = -3
 MIAIE_ENOMEM = -4
 MIAIE_EUNSUPPORTED = -5
+MIAIE_EFAULT = -6
 B_NN = 0
 B_NT = 1
 
@@ -67,6 +69,9 @@ _SIGS = {
     "miaie_copy_d2h": (_i, [_p, _p, _p, _sz]),
     "miaie_copy_d2d": (_i, [_p, _p, _p, _sz]),
     "miaie_wait": (_i, [_p, _i]),
+    "miaie_debug_device_checks": (_i, []),
+    "miaie_debug_register": (_i, [_p, _p, _sz]),
+    "miaie_debug_unregister": (_i, [_p, _p]),
     "miaie_mm_window_i32": (_i, [_p, _p, _p, _i]),
     "miaie_perf_window_u32": (_i, [_p, _p, _p, _i]),
     "miaie_dot_u8_probe": (_i, [_p, _p, _p]),
@@ -293,6 +298,16 @@ class Context:
 
     def wait(self, timeout_ms: int = -1) -> None:
         self._call("miaie_wait", timeout_ms)
+
+    # -- device bounds checks (the debug build; no-ops in the product build)
+    def device_checks(self) -> bool:
+        return bool(self.lib.miaie_debug_device_checks())
+
+    def debug_register(self, buf, nbytes: int) -> None:
+        self._call("miaie_debug_register", _addr(buf), _sz(nbytes))
+
+    def debug_unregister(self, buf) -> None:
+        self._call("miaie_debug_unregister", _addr(buf))
 
     def fill_i8(self, buf, n: int, tensor_id: int) -> None:
         self._call("miaie_fill_i8", _addr(buf), _sz(n), _u64(tensor_id))

@@ -9,6 +9,11 @@ harness/hlc/ through the hlc.py front end) and the measurement probes in
 aiehlc_amd/probes/.  Runs on a machine without a GPU
 (hipcc cross-compiles).
 
+The same sources are also built twice more: with host-side AddressSanitizer
+and UndefinedBehaviorSanitizer (aiehlc_amd/lib_san/), and with device-side
+bounds checks in every kernel (aiehlc_amd/lib_dbg/, MIAIE_DEVICE_CHECKS=1,
+csrc/dbg_checks.hpp).  A process selects either with MIAIE_LIB_DIR.
+
 Flags: -O3, C++17, hidden visibility (only the MIAIE_API symbols of
 include/miaie.h are exported), packed-FP32 instruction selection turned
 off (`-Xclang -target-feature -Xclang -packed-fp32-ops`), and kernel
@@ -27,6 +32,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 SANDIR = os.path.join(HERE, "lib_san")
+DBGDIR = os.path.join(HERE, "lib_dbg")
 LIB = os.path.join(LIBDIR, "libmiaie.so")
 HARNESS = os.path.join(HERE, "harness")
 XAIE_SRC = os.path.join(CSRC, "xaie")
@@ -82,6 +88,10 @@ def sources() -> list[str]:
 def build(verbose: bool = False, jobs: int | None = None) -> str:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
+    # the device-checked library's objects take longest (its int8 GEMM unit
+    # alone about 3.5 minutes): compile them beside everything else
+    dbg_pool = cf.ThreadPoolExecutor(2)
+    dbg_futs = _device_checked_objects(dbg_pool, verbose)
     srcs = sources()
     objs = [os.path.join(OBJ, os.path.basename(s)[:-4] + ".o") for s in srcs]
     jobs = jobs or min(8, len(srcs))
@@ -97,6 +107,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     build_hlc_samples(verbose)
     build_probes(verbose)
     build_sanitized(verbose, jobs)
+    for f in dbg_futs:
+        f.result()
+    dbg_pool.shutdown()
+    _link_device_checked(verbose)
     return LIB
 
 
@@ -123,6 +137,35 @@ def build_sanitized(verbose: bool = False, jobs: int | None = None) -> str:
           "-Wl,-rpath,$ORIGIN"], verbose)
     os.replace(xlib + ".tmp", xlib)
     return lib
+
+
+def _device_checked_objects(pool: cf.Executor, verbose: bool) -> list:
+    dobj = os.path.join(OBJ, "dbg")
+    os.makedirs(dobj, exist_ok=True)
+    # longest first (gemm_i8.hip)
+    srcs = sorted(sources(), key=lambda p: os.path.basename(p) != "gemm_i8.hip")
+    return [pool.submit(_run, [HIPCC, *HIP_FLAGS, "-DMIAIE_DEVICE_CHECKS=1", "-c", s,
+                               "-o", os.path.join(dobj, os.path.basename(s)[:-4] + ".o")], verbose) for s in srcs]
+
+
+def _link_device_checked(verbose: bool) -> str:
+    os.makedirs(DBGDIR, exist_ok=True)
+    dobj = os.path.join(OBJ, "dbg")
+    objs = [os.path.join(dobj, os.path.basename(s)[:-4] + ".o") for s in sources()]
+    lib = os.path.join(DBGDIR, "libmiaie.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", lib + ".tmp", *objs], verbose)
+    os.replace(lib + ".tmp", lib)
+    return lib
+
+
+def build_device_checked(verbose: bool = False, jobs: int | None = None) -> str:
+    """aiehlc_amd/lib_dbg/libmiaie.so: the same library with device-side
+    bounds checks (MIAIE_DEVICE_CHECKS=1, csrc/dbg_checks.hpp): every global
+    access of every kernel is checked against the runtime's buffer table."""
+    with cf.ThreadPoolExecutor(jobs or 8) as pool:
+        for f in _device_checked_objects(pool, verbose):
+            f.result()
+    return _link_device_checked(verbose)
 
 
 def build_xaie(verbose: bool = False) -> str:

@@ -95,13 +95,13 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
         const int r = rs / S, s = rs - r * S;
         const int koff = rs * Cin + cib * 32;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) wf[u][cb] = *reinterpret_cast<const v4i*>(wrow[cb] + koff);
+        for (int cb = 0; cb < 2; ++cb) wf[u][cb] = MIAIE_LD(reinterpret_cast<const v4i*>(wrow[cb] + koff));
 #pragma unroll
         for (int pb = 0; pb < 2; ++pb) {
           const int hi = phb[pb] + r, wi = pwb[pb] + s;
           const bool ok = pvalid[pb] && hi >= 0 && hi < H && wi >= 0 && wi < Wd;
           const int8_t* src = X + (((size_t)pn[pb] * H + hi) * Wd + wi) * Cin + cib * 32 + 16 * fh;
-          xf[u][pb] = ok ? *reinterpret_cast<const v4i*>(src) : v4i{0};
+          xf[u][pb] = ok ? MIAIE_LD(reinterpret_cast<const v4i*>(src)) : v4i{0};
         }
       }
     }
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
     int32_t* const dst = psum + ((size_t)blockIdx.z * P + p0 + p) * Cout + co0 + c16;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      *reinterpret_cast<v4i*>(dst + 4 * q) = v4i{sum[4 * q], sum[4 * q + 1], sum[4 * q + 2], sum[4 * q + 3]};
+      MIAIE_ST(reinterpret_cast<v4i*>(dst + 4 * q), (v4i{sum[4 * q], sum[4 * q + 1], sum[4 * q + 2], sum[4 * q + 3]}));
     return;
   }
   uint32_t out[4];
@@ -162,11 +162,11 @@ __global__ __launch_bounds__(256) void conv2d_i8_igemm(
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int c = co0 + c16 + 4 * q + t;
-      v |= (uint32_t)(requant1(sum[4 * q + t], shifts[c]) & 0xFF) << (8 * t);
+      v |= (uint32_t)(requant1(sum[4 * q + t], MIAIE_LD(shifts + c)) & 0xFF) << (8 * t);
     }
     out[q] = v;
   }
-  *reinterpret_cast<uint4*>(Y + (size_t)(p0 + p) * Cout + co0 + c16) = make_uint4(out[0], out[1], out[2], out[3]);
+  MIAIE_ST(reinterpret_cast<uint4*>(Y + (size_t)(p0 + p) * Cout + co0 + c16), make_uint4(out[0], out[1], out[2], out[3]));
 }
 
 // ------------------------------------------------------------ taps kernel
@@ -286,6 +286,7 @@ __global__ __launch_bounds__(256) void conv2d_i8_taps(
     at_issue = Tap{rs / S, rs % S, sb % CB};
     at_use = at_issue;
   }
+  const miaie::dbg::Span x_span = miaie::dbg::span_of(X), w_span = miaie::dbg::span_of(W);  // (debug build only)
   // copies of the stage at `t` into ring slot `slot`
   auto issue = [&](const Tap& t, int slot) {
     const uint32_t base = lds0 + slot * G::STAGE + 1024 * wave;
@@ -296,9 +297,9 @@ __global__ __launch_bounds__(256) void conv2d_i8_taps(
     for (int i = 0; i < (G::CPX > G::CPW ? G::CPX : G::CPW); ++i) {
       if (i < G::CPX) {
         const int hi = min(max(xhb[i] + t.r, 0), H - 1), wi = min(max(xwb[i] + t.s, 0), Wd - 1);
-        miaie::dev::gload_lds16(X, xbase[i] + (uint32_t)hi * rowx + (uint32_t)wi * Cin + xk, base + 4096 * i);
+        miaie::dev::gload_lds16(X, xbase[i] + (uint32_t)hi * rowx + (uint32_t)wi * Cin + xk, base + 4096 * i, x_span);
       }
-      if (i < G::CPW) miaie::dev::gload_lds16(W, wbase[i] + wk, base + G::XB + 4096 * i);
+      if (i < G::CPW) miaie::dev::gload_lds16(W, wbase[i] + wk, base + G::XB + 4096 * i, w_span);
     }
   };
 
@@ -363,8 +364,8 @@ __global__ __launch_bounds__(256) void conv2d_i8_taps(
         int32_t* const dst = psum + ((size_t)blockIdx.z * P + pf) * Cout + co0 + TC / 2 * cb + 32 * j + 4 * fh;
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<v4i*>(dst + 8 * g) =
-              v4i{acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]};
+          MIAIE_ST(reinterpret_cast<v4i*>(dst + 8 * g),
+                   (v4i{acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]}));
       }
     }
     return;
@@ -377,7 +378,7 @@ __global__ __launch_bounds__(256) void conv2d_i8_taps(
     const int cl = 32 * j + 4 * fh;  // channel within the wave's half
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const uint32_t sh = *reinterpret_cast<const uint32_t*>(shifts + co0 + TC / 2 * cb + cl + 8 * g);
+      const uint32_t sh = MIAIE_LD(reinterpret_cast<const uint32_t*>(shifts + co0 + TC / 2 * cb + cl + 8 * g));
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         uint32_t v = 0;
@@ -397,7 +398,7 @@ __global__ __launch_bounds__(256) void conv2d_i8_taps(
     const int p = p0 + TP / 2 * pb + sp;
     if (p < P) {
       const v4i v = *reinterpret_cast<const v4i*>(yb + sp * G::YP + 16 * ch);
-      *reinterpret_cast<v4i*>(Y + (size_t)p * Cout + co0 + TC / 2 * cb + 16 * ch) = v;
+      MIAIE_ST(reinterpret_cast<v4i*>(Y + (size_t)p * Cout + co0 + TC / 2 * cb + 16 * ch), v);
     }
   }
 }
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(256) void conv2d_i8_splitk_reduce(const int32_t* __
   for (int z = 0; z < ksplit; ++z) {
     const int32_t* src = part + (size_t)z * PC + e;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) s[q] += *reinterpret_cast<const v4i*>(src + 4 * q);
+    for (int q = 0; q < 4; ++q) s[q] += MIAIE_LD(reinterpret_cast<const v4i*>(src + 4 * q));
   }
   const int c0 = (int)(e % Cout);
   uint32_t out[4];
@@ -423,10 +424,10 @@ __global__ __launch_bounds__(256) void conv2d_i8_splitk_reduce(const int32_t* __
   for (int q = 0; q < 4; ++q) {
     uint32_t v = 0;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) v |= (uint32_t)(requant1(s[q][t], shifts[c0 + 4 * q + t]) & 0xFF) << (8 * t);
+    for (int t = 0; t < 4; ++t) v |= (uint32_t)(requant1(s[q][t], MIAIE_LD(shifts + c0 + 4 * q + t)) & 0xFF) << (8 * t);
     out[q] = v;
   }
-  *reinterpret_cast<uint4*>(Y + e) = make_uint4(out[0], out[1], out[2], out[3]);
+  MIAIE_ST(reinterpret_cast<uint4*>(Y + e), make_uint4(out[0], out[1], out[2], out[3]));
 }
 
 // Any-shape fallback: one thread per output element.
@@ -452,10 +453,10 @@ __global__ __launch_bounds__(256) void conv2d_i8_direct(const int8_t* __restrict
       if (wi < 0 || wi >= Wd) continue;
       const int8_t* x = X + (((size_t)n * H + hi) * Wd + wi) * Cin;
       const int8_t* w = W + (((size_t)co * R + r) * S + s) * Cin;
-      for (int ci = 0; ci < Cin; ++ci) acc += (uint32_t)((int)x[ci] * (int)w[ci]);
+      for (int ci = 0; ci < Cin; ++ci) acc += (uint32_t)((int)MIAIE_LD(x + ci) * (int)MIAIE_LD(w + ci));
     }
   }
-  Y[idx] = (int8_t)requant1((int)acc, shifts[co]);
+  MIAIE_ST(Y + idx, (int8_t)requant1((int)acc, MIAIE_LD(shifts + co)));
 }
 
 }  // namespace

@@ -35,6 +35,7 @@
 
 #include <type_traits>
 
+#include "dbg_checks.hpp"
 #include "miaie_internal.hpp"
 
 namespace miaie {
@@ -121,7 +122,7 @@ __device__ __forceinline__ void rows_epilogue(const v16i& acc, const uint32_t (&
   const int sp = 32 * pb + (lane >> 1), sh = lane & 1;
   if (wc0 + sp < Wo && ho0 + rr < Ho) {
     const v4i v = *reinterpret_cast<const v4i*>(ys + (rr * G::BW_ + sp) * G::YP + 32 * wc + 16 * sh);
-    *reinterpret_cast<v4i*>(Y + (uint32_t)(((n * Ho + ho0 + rr) * Wo + wc0 + sp) * Cout + co0 + 32 * wc + 16 * sh)) = v;
+    MIAIE_ST(reinterpret_cast<v4i*>(Y + (uint32_t)(((n * Ho + ho0 + rr) * Wo + wc0 + sp) * Cout + co0 + 32 * wc + 16 * sh)), v);
   }
 }
 
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   // their latency hides under the staging
   uint32_t sh4[4];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) sh4[g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc + 8 * g + 4 * fh);
+  for (int g = 0; g < 4; ++g) sh4[g] = MIAIE_LD(reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc + 8 * g + 4 * fh));
 
   // ---- stage X (zero outside the image) and W.  Every load is issued before
   // any is waited for: positions outside the image load the nearest chunk
@@ -204,12 +205,12 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   auto xrow_of = [&](int u) { return min(G::RPP * u + xrow, G::XR - 1); };
 #pragma unroll
   for (int u = 0; u < G::XQ; ++u)
-    xv[u] = *reinterpret_cast<const v4i*>(X + x_off(xrow_of(u), xcol, xc, xin[u]));
-  xe = *reinterpret_cast<const v4i*>(X + x_off(erow, ecol, ec, ein));
+    xv[u] = MIAIE_LD(reinterpret_cast<const v4i*>(X + x_off(xrow_of(u), xcol, xc, xin[u])));
+  xe = MIAIE_LD(reinterpret_cast<const v4i*>(X + x_off(erow, ecol, ec, ein)));
   // (threads past the end of the last W pass repeat that pass's chunks)
   auto wq_of = [&](int u) { return u < G::WQ - 1 ? tid + 512 * u : 512 * (G::WQ - 1) + tid % G::WREM; };
 #pragma unroll
-  for (int u = 0; u < G::WQ; ++u) wv[u] = *reinterpret_cast<const v4i*>(W + (uint32_t)(co0 * G::RSC + 16 * wq_of(u)));
+  for (int u = 0; u < G::WQ; ++u) wv[u] = MIAIE_LD(reinterpret_cast<const v4i*>(W + (uint32_t)(co0 * G::RSC + 16 * wq_of(u))));
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
 
   // The accumulators start at the rounding term 2^(s-1) of their channel
@@ -370,10 +371,10 @@ __global__ __launch_bounds__(512) void conv2d_i8_rowsk(const int8_t* __restrict_
   auto load = [&](int kc) {
     const uint64_t k0 = (uint64_t)(kc * CK);
 #pragma unroll
-    for (int u = 0; u < G::XQ; ++u) xv[u] = *reinterpret_cast<const v4i*>(X + xo[u] + k0);
-    xe = *reinterpret_cast<const v4i*>(X + eo + k0);
+    for (int u = 0; u < G::XQ; ++u) xv[u] = MIAIE_LD(reinterpret_cast<const v4i*>(X + xo[u] + k0));
+    xe = MIAIE_LD(reinterpret_cast<const v4i*>(X + eo + k0));
 #pragma unroll
-    for (int u = 0; u < G::WQ; ++u) wv[u] = *reinterpret_cast<const v4i*>(W + wo[u] + k0);
+    for (int u = 0; u < G::WQ; ++u) wv[u] = MIAIE_LD(reinterpret_cast<const v4i*>(W + wo[u] + k0));
   };
   // Write load i (in issue order: X passes, the last columns, W passes) of
   // the staged chunk into LDS buffer buf.
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(512) void conv2d_i8_rowsk(const int8_t* __restrict_
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      sh4[j][g] = *reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * (NJ * wj + j) + 8 * g + 4 * fh);
+      sh4[j][g] = MIAIE_LD(reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * (NJ * wj + j) + 8 * g + 4 * fh));
   const int nk = Cin / CK;
   load(0);
   __builtin_amdgcn_sched_barrier(0);

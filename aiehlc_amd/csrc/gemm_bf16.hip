@@ -27,6 +27,7 @@
 namespace {
 
 namespace dev = miaie::dev;
+namespace dbg = miaie::dbg;
 
 // 64-byte LDS rows: chunk c of row r at chunk c ^ swz(r).  gfx950 serves a
 // ds_read_b128 16 lanes at a time from 64 four-byte banks; XOR with row
@@ -50,6 +51,7 @@ __device__ __forceinline__ v8bf as_bf(v4i x) { return __builtin_bit_cast(v8bf, x
 __device__ __forceinline__ void store_tile_f32(const v16f (&acc)[4][4], int8_t* lds, int wave, int lane, float* C,
                                                int m0, int n0, int N) {
   const int wm = wave >> 1, wn = wave & 1, fr = lane & 31, fh = lane >> 5;
+  const dbg::Span c_span = dbg::span_of(C);  // (debug build only)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     dev::barrier();  // the other waves' last reads of this LDS (k-loop fragments or the previous half)
@@ -71,7 +73,7 @@ __device__ __forceinline__ void store_tile_f32(const v16f (&acc)[4][4], int8_t* 
       const int R = wave * 32 + rr;
       const v4f v = *reinterpret_cast<const v4f*>(lds + R * 1024 + ((lane ^ (R & 15)) << 4));
       const int m = m0 + (R >> 6) * 128 + 64 * h + (R & 63);
-      __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(C + (size_t)m * N + n0 + 4 * lane));
+      MIAIE_ST_NT_IN(c_span, reinterpret_cast<v4f*>(C + (size_t)m * N + n0 + 4 * lane), v);
     }
   }
 }
@@ -117,14 +119,15 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_tile256(const uint16_t* __re
   const int b_r = 2 * wave + (lane >> 5);  // (b_r + 8i) & 3 == b_r & 3
   const uint32_t b_voff = (uint32_t)(b_r * ldb) + 16 * ((lane & 31) ^ ((b_r & 3) << 2));
   const int8_t* const b_base = reinterpret_cast<const int8_t*>(B) + (size_t)n0 * 2;
+  const dbg::Span a_span = dbg::span_of(A), b_span = dbg::span_of(B);  // (debug build only)
 
   auto issue = [&](int kt, int stage, int i) {
     const uint32_t st = lds0 + stage * STAGE_BYTES + 1024 * wave;
     if (i < 4)
-      dev::gload_lds16(a_base + (size_t)kt * BK * 2 + (size_t)(64 * i) * lda, a_voff, st + 4096 * i);
+      dev::gload_lds16(a_base + (size_t)kt * BK * 2 + (size_t)(64 * i) * lda, a_voff, st + 4096 * i, a_span);
     else
       dev::gload_lds16(b_base + (size_t)kt * BK * ldb + (size_t)(8 * (i - 4)) * ldb, b_voff,
-                       st + TILE_BYTES + 4096 * (i - 4));
+                       st + TILE_BYTES + 4096 * (i - 4), b_span);
   };
 
   // fragment offsets within a stage
@@ -312,7 +315,12 @@ static_assert(PAIR_LDS <= 163840, "pair-staged LDS budget");
 __device__ __forceinline__ int bswz16(int k) { return ((k & 3) << 2) | (((k >> 3) & 1) << 1); }
 
 __device__ __forceinline__ void mfma16_bf16(v4f& acc, v4i a, v4i b) {
+#if MIAIE_DEVICE_CHECKS
+  // debug build: the compiler's own MFMA, whose hazards it tracks (see mfma16)
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(a), as_bf(b), acc, 0, 0, 0);
+#else
   asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+#endif
 }
 
 // fp32 epilogue of a 256x256 tile held as acc[i][j][e] = C[m0 + wm*128 + 16i +
@@ -323,6 +331,7 @@ __device__ __forceinline__ void mfma16_bf16(v4f& acc, v4i a, v4i b) {
 __device__ __forceinline__ void store_tile16_f32(const v4f (&acc)[8][8], int8_t* lds, int wave, int lane, float* C,
                                                  int m0, int n0, int N) {
   const int wm = wave >> 1, wn = wave & 1, fr = lane & 15, fg = lane >> 4;
+  const dbg::Span c_span = dbg::span_of(C);  // (debug build only)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     dev::barrier();  // the other waves' last reads of this LDS
@@ -340,7 +349,7 @@ __device__ __forceinline__ void store_tile16_f32(const v4f (&acc)[8][8], int8_t*
       const int R = wave * 32 + rr;
       const v4f v = *reinterpret_cast<const v4f*>(lds + R * 1024 + ((lane ^ (R & 15)) << 4));
       const int m = m0 + (R >> 6) * 128 + 64 * h + (R & 63);
-      __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(C + (size_t)m * N + n0 + 4 * lane));
+      MIAIE_ST_NT_IN(c_span, reinterpret_cast<v4f*>(C + (size_t)m * N + n0 + 4 * lane), v);
     }
   }
 }
@@ -375,11 +384,12 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_pair16(const uint16_t* __res
   const int8_t* const b_base = reinterpret_cast<const int8_t*>(B) + (size_t)n0 * 2;
   const size_t b_kstep = (size_t)BK * ldb;
   const uint32_t ldsw = lds0 + 1024 * wave;
+  const dbg::Span a_span = dbg::span_of(A), b_span = dbg::span_of(B);  // (debug build only)
   auto copy_a = [&](const int8_t* src, uint32_t st, int x) __attribute__((always_inline)) {
-    dev::gload_lds16(src + (size_t)(32 * x) * lda, a_voff, ldsw + B_REGION + st + 4096 * x);
+    dev::gload_lds16(src + (size_t)(32 * x) * lda, a_voff, ldsw + B_REGION + st + 4096 * x, a_span);
   };
   auto copy_b = [&](const int8_t* src, uint32_t st, int x) __attribute__((always_inline)) {
-    dev::gload_lds16(src + (size_t)(8 * x) * ldb, b_voff[x & 1], ldsw + st + 4096 * x);
+    dev::gload_lds16(src + (size_t)(8 * x) * ldb, b_voff[x & 1], ldsw + st + 4096 * x, b_span);
   };
 
   const int wm = wave >> 1, wn = wave & 1;
@@ -567,7 +577,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restri
       const int m = m0 + row, k = k0 + ch * 8;
       uint16_t tmp[8];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) tmp[t] = (m < M && k + t < K) ? A[(size_t)m * K + k + t] : 0;
+      for (int t = 0; t < 8; ++t) tmp[t] = (m < M && k + t < K) ? MIAIE_LD(A + (size_t)m * K + k + t) : 0;
       v4i v;
       __builtin_memcpy(&v, tmp, 16);
       *reinterpret_cast<v4i*>(as + lds_off(row, ch)) = v;
@@ -579,7 +589,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restri
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const int k = k0 + ch * 8 + t;
-        tmp[t] = (n < N && k < K) ? B[(size_t)k * N + n] : 0;
+        tmp[t] = (n < N && k < K) ? MIAIE_LD(B + (size_t)k * N + n) : 0;
       }
       v4i v;
       __builtin_memcpy(&v, tmp, 16);
@@ -599,7 +609,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64(const uint16_t* __restri
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int n = n0 + wn * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
-    if (n < N) C[(size_t)m * N + n] = acc[e];
+    if (n < N) MIAIE_ST(C + (size_t)m * N + n, acc[e]);
   }
 }
 
@@ -625,11 +635,11 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64p(const uint16_t* __restr
   const uint16_t* const a_p = A + (size_t)min(m0 + row, M - 1) * K;
   const uint16_t* const b_p = B + min(n0 + col, N - 1);
   auto load = [&](int k0, v4i& va, v4i& vb) {
-    va = *reinterpret_cast<const v4i*>(a_p + min(k0 + 8 * ch, K - 8));
+    va = MIAIE_LD(reinterpret_cast<const v4i*>(a_p + min(k0 + 8 * ch, K - 8)));
     const uint16_t* const p = b_p + (size_t)min(k0 + 8 * bch, K - 8) * N;
     uint16_t tmp[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) tmp[t] = p[(size_t)t * N];
+    for (int t = 0; t < 8; ++t) tmp[t] = MIAIE_LD(p + (size_t)t * N);
     __builtin_memcpy(&vb, tmp, 16);
   };
   v16f acc = v16f{0.f};
@@ -653,7 +663,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_tile64p(const uint16_t* __restr
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int n = n0 + wn * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
-    if (n < N) C[(size_t)m * N + n] = acc[e];
+    if (n < N) MIAIE_ST(C + (size_t)m * N + n, acc[e]);
   }
 }
 

@@ -69,11 +69,11 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64(const int8_t* __restrict__
       if (m < M) {
         const int8_t* p = A + (size_t)m * lda + k;
         if (k + 16 <= K && miaie::aligned(p, 16)) {
-          v = *reinterpret_cast<const v4i*>(p);
+          v = MIAIE_LD(reinterpret_cast<const v4i*>(p));
         } else {
           int8_t tmp[16];
 #pragma unroll
-          for (int t = 0; t < 16; ++t) tmp[t] = (k + t < K) ? p[t] : 0;
+          for (int t = 0; t < 16; ++t) tmp[t] = (k + t < K) ? MIAIE_LD(p + t) : 0;
           __builtin_memcpy(&v, tmp, 16);
         }
       }
@@ -86,11 +86,11 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64(const int8_t* __restrict__
       if (n < N) {
         const int8_t* p = B + (size_t)n * ldb + k;
         if (k + 16 <= K && miaie::aligned(p, 16)) {
-          v = *reinterpret_cast<const v4i*>(p);
+          v = MIAIE_LD(reinterpret_cast<const v4i*>(p));
         } else {
           int8_t tmp[16];
 #pragma unroll
-          for (int t = 0; t < 16; ++t) tmp[t] = (k + t < K) ? p[t] : 0;
+          for (int t = 0; t < 16; ++t) tmp[t] = (k + t < K) ? MIAIE_LD(p + t) : 0;
           __builtin_memcpy(&v, tmp, 16);
         }
       }
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64(const int8_t* __restrict__
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
         const int k = k0 + ch * 16 + t;
-        tmp[t] = (n < N && k < K) ? B[(size_t)k * ldb + n] : 0;
+        tmp[t] = (n < N && k < K) ? MIAIE_LD(B + (size_t)k * ldb + n) : 0;
       }
       v4i v;
       __builtin_memcpy(&v, tmp, 16);
@@ -125,8 +125,8 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64(const int8_t* __restrict__
   for (int e = 0; e < 16; ++e) {
     const int n = n0 + wn * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
     if (n < N) {
-      if (C) C[(size_t)m * ldc + n] = acc[e];
-      if (Y) Y[(size_t)m * ldy + n] = (int8_t)requant1(acc[e], shift, relu);
+      if (C) MIAIE_ST(C + (size_t)m * ldc + n, acc[e]);
+      if (Y) MIAIE_ST(Y + (size_t)m * ldy + n, (int8_t)requant1(acc[e], shift, relu));
     }
   }
 }
@@ -163,14 +163,14 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64p(const int8_t* __restrict_
   const int bk = B_NT ? ch : bch;  // this thread's k-chunk of B
 
   auto load = [&](int k0, v4i& va, v4i& vb) {
-    va = *reinterpret_cast<const v4i*>(a_p + min(k0 + 16 * ch, K - 16));
+    va = MIAIE_LD(reinterpret_cast<const v4i*>(a_p + min(k0 + 16 * ch, K - 16)));
     if constexpr (B_NT) {
-      vb = *reinterpret_cast<const v4i*>(b_p + min(k0 + 16 * ch, K - 16));
+      vb = MIAIE_LD(reinterpret_cast<const v4i*>(b_p + min(k0 + 16 * ch, K - 16)));
     } else {
       const int8_t* const p = b_p + (size_t)min(k0 + 16 * bch, K - 16) * ldb;
       int8_t tmp[16];
 #pragma unroll
-      for (int t = 0; t < 16; ++t) tmp[t] = p[(size_t)t * ldb];
+      for (int t = 0; t < 16; ++t) tmp[t] = MIAIE_LD(p + (size_t)t * ldb);
       __builtin_memcpy(&vb, tmp, 16);
     }
   };
@@ -201,8 +201,8 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64p(const int8_t* __restrict_
   for (int e = 0; e < 16; ++e) {
     const int n = n0 + wn * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
     if (n < N) {
-      if (C) C[(size_t)m * ldc + n] = acc[e];
-      if (Y) Y[(size_t)m * ldy + n] = (int8_t)requant1(acc[e], shift, relu);
+      if (C) MIAIE_ST(C + (size_t)m * ldc + n, acc[e]);
+      if (Y) MIAIE_ST(Y + (size_t)m * ldy + n, (int8_t)requant1(acc[e], shift, relu));
     }
   }
 }

@@ -170,6 +170,7 @@ __device__ __forceinline__ void pipe_epilogue(v16i (&acc)[NI][NJ], int8_t* lds, 
                                               int32_t* __restrict__ C, int ldy, int ldc, int shift, int relu,
                                               int rnd_add) {
   constexpr int WM = BM / 2, WN = BN / (NW / 2), THREADS = 64 * NW;
+  const dbg::Span y_span = dbg::span_of(Y), c_span = dbg::span_of(C);  // (debug build only)
   if constexpr (WRITE_C) {
 #pragma unroll
     for (int i = 0; i < NI; ++i)
@@ -180,7 +181,7 @@ __device__ __forceinline__ void pipe_epilogue(v16i (&acc)[NI][NJ], int8_t* lds, 
           const int m = m0 + wm * WM + 32 * i + fr;
           const int n = n0 + wn * WN + 32 * j + 8 * g + 4 * fh;
           v4i v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(C + (size_t)m * ldc + n));
+          MIAIE_ST_NT_IN(c_span, reinterpret_cast<v4i*>(C + (size_t)m * ldc + n), v);
         }
   }
   if constexpr (YQ != Y_NONE) {
@@ -217,7 +218,7 @@ __device__ __forceinline__ void pipe_epilogue(v16i (&acc)[NI][NJ], int8_t* lds, 
         const int ml = flat / CH, c = flat % CH;
         const int m = (ml / 32) * WM + 32 * i + (ml % 32);  // row within the tile
         const v4i v = *reinterpret_cast<const v4i*>(buf + ml * BN + ((c ^ (ml & (CH - 1))) << 4));
-        __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + c * 16));
+        MIAIE_ST_NT_IN(y_span, reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + c * 16), v);
       }
     };
     auto run = [&](const auto& rq) {
@@ -280,6 +281,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
   const int a_r = 16 * wave + (lane >> 2);
   const uint32_t a_voff = (uint32_t)a_r * lda + 16 * ((lane & 3) ^ swz(a_r));  // swz(a_r + 16*NW*i) == swz(a_r)
   const int8_t* const a_base = A + (size_t)m0 * lda;
+  const dbg::Span a_span = dbg::span_of(A), b_span = dbg::span_of(B);  // (debug build only)
   uint32_t b_voff;
   const int8_t* b_base;
   constexpr int B_ROWS_PER_CP = B_NT ? 16 * NW : 1024 * NW / BN;  // operand rows between copies i and i+1
@@ -297,11 +299,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_i8_pipe(
   auto copy = [&](int kt, int stage, int x) {
     const uint32_t st = lds0 + stage * G::STAGE_BYTES + 1024 * wave;
     if (x < G::A_CP) {
-      dev::gload_lds16(a_base + (size_t)kt * BK + (size_t)(16 * NW * x) * lda, a_voff, st + G::CP_BYTES * x);
+      dev::gload_lds16(a_base + (size_t)kt * BK + (size_t)(16 * NW * x) * lda, a_voff, st + G::CP_BYTES * x, a_span);
     } else {
       const int i = x - G::A_CP;
       const int8_t* bb = B_NT ? b_base + (size_t)kt * BK : b_base + (size_t)kt * BK * ldb;
-      dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * i) * ldb, b_voff, st + G::A_BYTES + G::CP_BYTES * i);
+      dev::gload_lds16(bb + (size_t)(B_ROWS_PER_CP * i) * ldb, b_voff, st + G::A_BYTES + G::CP_BYTES * i, b_span);
     }
   };
 
@@ -566,7 +568,14 @@ __device__ __forceinline__ int bswz16(int k) {
 // main loop waits out the last MFMAs' latency before any accumulator is read
 // (mfma16_drain).
 __device__ __forceinline__ void mfma16(v4i& acc, v4i a, v4i b) {
+#if MIAIE_DEVICE_CHECKS
+  // debug build: the checks' extra registers let the compiler move
+  // accumulators inside the loop, so it gets its own MFMA, whose hazards it
+  // tracks (slower, same sums)
+  acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+#else
   asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+#endif
 }
 // 8-pass MFMA results are readable by VALU after 11 wait states (gfx950);
 // 24 here, with nothing scheduled across.
@@ -633,16 +642,17 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int m0, int n0, const i
   }
   const int8_t* const a_base = A + (size_t)m0 * lda;
   const int8_t* const b_base = B_NT ? B + (size_t)n0 * ldb : B + n0;
+  const dbg::Span a_span = dbg::span_of(A), b_span = dbg::span_of(B);  // (debug build only)
   const size_t b_kstep = B_NT ? (size_t)BK : (size_t)BK * ldb;  // B source per k-tile
   const uint32_t ldsw = lds0 + 1024 * wave;
   // copy x of an A pair (source src) into the pair stage at byte st of the A region
   auto copy_a = [&](const int8_t* src, uint32_t st, int x) __attribute__((always_inline)) {
-    dev::gload_lds16(src + (size_t)(8 * NW * x) * lda, a_voff, ldsw + B_REGION + st + G::CP_BYTES * x);
+    dev::gload_lds16(src + (size_t)(8 * NW * x) * lda, a_voff, ldsw + B_REGION + st + G::CP_BYTES * x, a_span);
   };
   // copy x of a B k-tile (source src) into the B stage at byte st
   auto copy_b = [&](const int8_t* src, uint32_t st, int x) __attribute__((always_inline)) {
     dev::gload_lds16(src + (size_t)(B_ROWS_PER_CP * x) * ldb, b_voff[B_ROWS_PER_CP == 16 ? (x & 1) : 0],
-                     ldsw + st + G::CP_BYTES * x);
+                     ldsw + st + G::CP_BYTES * x, b_span);
   };
 
   // ---- fragments.  A fragment i of k-tile 2p + par: row wm*WM + 16i +
@@ -859,6 +869,7 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int m0, int n0, const i
   // ---- epilogue.  acc[i][j][e]: row wm*WM + 16i + lane%16, column
   // wn*WN + 16j + 4(lane/16) + e.
   constexpr int WM = H::WM, WN = H::WN, THREADS = 64 * NW;
+  const dbg::Span y_span = dbg::span_of(Y), c_span = dbg::span_of(C);  // (debug build only)
   const int rnd_add = rnd - acc0;
   if constexpr (WRITE_C) {
 #pragma unroll
@@ -867,7 +878,7 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int m0, int n0, const i
       for (int j = 0; j < NJ; ++j) {
         const int m = m0 + wm * WM + 16 * i + fr;
         const int n = n0 + wn * WN + 16 * j + 4 * fg;
-        __builtin_nontemporal_store(acc[i][j], reinterpret_cast<v4i*>(C + (size_t)m * ldc + n));
+        MIAIE_ST_NT_IN(c_span, reinterpret_cast<v4i*>(C + (size_t)m * ldc + n), acc[i][j]);
       }
   }
   if constexpr (WRITE_Y) {
@@ -898,9 +909,9 @@ __device__ __forceinline__ void pipe16_tile(int8_t* lds, int m0, int n0, const i
         const v4i v = *reinterpret_cast<const v4i*>(buf + ml * BN + ((ch ^ (ml & (CH - 1))) << 4));
         v4i* const dst = reinterpret_cast<v4i*>(Y + (size_t)(m0 + m) * ldy + n0 + ch * 16);
         if constexpr (KEEP_Y)
-          *dst = v;
+          MIAIE_ST_IN(y_span, dst, v);
         else
-          __builtin_nontemporal_store(v, dst);
+          MIAIE_ST_NT_IN(y_span, dst, v);
       }
     };
     auto run = [&](const auto& rq) {

@@ -6,6 +6,8 @@
 
 #include <cstdint>
 
+#include "dbg_checks.hpp"
+
 #define MIAIE_LDS __attribute__((address_space(3)))
 
 typedef int miaie_v2i __attribute__((ext_vector_type(2)));
@@ -27,7 +29,23 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // the copy (it would put a vmcnt(0) in front of each); callers therefore
 // wait for their own copies with wait_vmcnt<N>() before the barrier that
 // publishes them.  m0 must be wave-uniform.
-__device__ __forceinline__ void gload_lds16(const void* sbase, uint32_t voff, uint32_t m0) {
+// (In the debug build a lane whose 16 bytes lie outside `span`, the buffer
+// of the copied operand, is left out of the copy and reported; line is the
+// caller's.  In the product build span is empty and unused.)
+__device__ __forceinline__ void gload_lds16(const void* sbase, uint32_t voff, uint32_t m0, dbg::Span span,
+                                            int line = __builtin_LINE(),
+                                            uint32_t file = dbg::file_id(__builtin_FILE_NAME())) {
+#if MIAIE_DEVICE_CHECKS
+  const void* p = static_cast<const char*>(sbase) + voff;
+  if (!dbg::in_span(span, p, 16)) {
+    dbg::report(p, 16, 2, line, file);
+    return;
+  }
+#else
+  (void)span;
+  (void)line;
+  (void)file;
+#endif
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 

@@ -8,6 +8,7 @@
 #include <cstdio>
 
 #include "../../include/miaie.h"
+#include "dbg_checks.hpp"
 
 struct miaie_ctx {
   unsigned long long id = 0;  // unique per context in the process (a graph records its context's id)
@@ -47,6 +48,15 @@ int check_launch(miaie_ctx* ctx, const char* kernel);
 int refuse_while_recording(miaie_ctx* ctx, const char* what);
 
 __host__ __device__ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// The device-check buffer table of the debug build (no-ops returning
+// MIAIE_OK in the product build; miaie_runtime.hip): add or replace the
+// extent of the buffer at p, drop it, and read (and clear) the fault records
+// after the context's stream has drained (MIAIE_EFAULT with a message naming
+// the first fault).
+int dbg_add(miaie_ctx* ctx, const void* p, size_t bytes);
+int dbg_remove(miaie_ctx* ctx, const void* p);
+int dbg_take_faults(miaie_ctx* ctx);
 
 // Resolve the device address of the allocation-free entry points' scratch
 // array on ctx->device (current) into ctx->scratch (noalloc.hip).

@@ -11,6 +11,9 @@
 
 #include <atomic>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <vector>
 
 #include "miaie_internal.hpp"
 
@@ -53,6 +56,109 @@ int refuse_while_recording(miaie_ctx* ctx, const char* what) {
   return MIAIE_OK;
 }
 
+// ---------------------------------------------------------------- device bounds checks
+// The buffer table of the debug build (dbg_checks.hpp): one process-wide map
+// of [lo, hi) ranges, uploaded into every translation unit's copy of the
+// device table on the context's device after each change.  The product build
+// keeps nothing: the hooks below return MIAIE_OK.
+#if MIAIE_DEVICE_CHECKS
+namespace dbg {
+namespace {
+std::mutex& table_mu() {
+  static std::mutex m;
+  return m;
+}
+std::vector<Unit>& units() {
+  static std::vector<Unit> u;
+  return u;
+}
+std::map<uint64_t, uint64_t>& table() {
+  static std::map<uint64_t, uint64_t> t;
+  return t;
+}
+// with table_mu held
+int upload_locked(miaie_ctx* ctx) {
+  static Ranges r;
+  r.n = 0;
+  for (const auto& [lo, hi] : table()) {
+    r.lo[r.n] = lo;
+    r.hi[r.n] = hi;
+    ++r.n;
+  }
+  // kernels in flight read the table: replace it only when the device is idle
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipDeviceSynchronize (device check table)");
+  for (const Unit& u : units()) {
+    e = (hipError_t)u.upload(r, ctx->device);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipMemcpyToSymbol (device check table)");
+  }
+  return MIAIE_OK;
+}
+}  // namespace
+
+void register_unit(const Unit& u) {
+  std::lock_guard<std::mutex> lock(table_mu());
+  units().push_back(u);
+}
+}  // namespace dbg
+
+int dbg_add(miaie_ctx* ctx, const void* p, size_t bytes) {
+  std::lock_guard<std::mutex> lock(dbg::table_mu());
+  auto& t = dbg::table();
+  const uint64_t lo = (uint64_t)(uintptr_t)p, hi = lo + bytes;
+  t.erase(lo);  // a new extent for a known base replaces the old one
+  auto next = t.lower_bound(lo);
+  if (next != t.end() && next->first < hi)
+    return fail(ctx, MIAIE_EINVAL, "device check table: [%p, +%zu) overlaps the buffer at 0x%llx", p, bytes,
+                (unsigned long long)next->first);
+  if (next != t.begin() && std::prev(next)->second > lo)
+    return fail(ctx, MIAIE_EINVAL, "device check table: [%p, +%zu) overlaps the buffer at 0x%llx", p, bytes,
+                (unsigned long long)std::prev(next)->first);
+  if (t.size() >= (size_t)dbg::kMaxRanges)
+    return fail(ctx, MIAIE_ENOMEM, "device check table: more than %d buffers", dbg::kMaxRanges);
+  t[lo] = hi;
+  return dbg::upload_locked(ctx);
+}
+
+int dbg_remove(miaie_ctx* ctx, const void* p) {
+  std::lock_guard<std::mutex> lock(dbg::table_mu());
+  if (dbg::table().erase((uint64_t)(uintptr_t)p) == 0) return MIAIE_OK;
+  return dbg::upload_locked(ctx);
+}
+
+int dbg_take_faults(miaie_ctx* ctx) {
+  std::lock_guard<std::mutex> lock(dbg::table_mu());
+  unsigned long long total = 0;
+  dbg::Fault first{};
+  const char* where = "";
+  for (const dbg::Unit& u : dbg::units()) {
+    dbg::Fault f{};
+    hipError_t e = (hipError_t)u.take(&f, ctx->device);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipMemcpyFromSymbol (device check record)");
+    if (f.count && !total) {
+      first = f;
+      where = u.name;
+    }
+    total += f.count;
+  }
+  if (!total) return MIAIE_OK;
+  static const char* const kind[] = {"load", "store", "global->LDS copy"};
+  const char* file = nullptr;
+  for (const char* f : dbg::kFiles)
+    if (dbg::file_id(f) == first.file) file = f;
+  const char* base = std::strrchr(where, '/');
+  return fail(ctx, MIAIE_EFAULT,
+              "device bounds check: %llu access(es) outside every known buffer; first: %s of %llu bytes at 0x%llx "
+              "(%s, line %d; kernel from %s)",
+              total, kind[first.write >= 0 && first.write <= 2 ? first.write : 0], first.bytes, first.addr,
+              file ? file : "?", first.line, base ? base + 1 : where);
+}
+#else
+int dbg_add(miaie_ctx*, const void*, size_t) { return MIAIE_OK; }
+int dbg_remove(miaie_ctx*, const void*) { return MIAIE_OK; }
+int dbg_take_faults(miaie_ctx*) { return MIAIE_OK; }
+#endif
+
 }  // namespace miaie
 
 using namespace miaie;
@@ -76,9 +182,9 @@ __global__ __launch_bounds__(256) void copy_kernel(v4i* __restrict__ dst,
                                                    size_t ntail) {
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (; i < nvec; i += stride) dst[i] = __builtin_nontemporal_load(src + i);
+  for (; i < nvec; i += stride) MIAIE_ST(dst + i, MIAIE_LD_NT(src + i));
   size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (t < ntail) dst_tail[t] = src_tail[t];
+  if (t < ntail) MIAIE_ST(dst_tail + t, MIAIE_LD(src_tail + t));
 }
 
 // 16 seeded int8 values per thread.
@@ -98,9 +204,9 @@ __global__ __launch_bounds__(256) void fill_i8_kernel(int8_t* __restrict__ dst, 
       }
       w[q] = v;
     }
-    *reinterpret_cast<uint4*>(dst + base) = make_uint4(w[0], w[1], w[2], w[3]);
+    MIAIE_ST(reinterpret_cast<uint4*>(dst + base), make_uint4(w[0], w[1], w[2], w[3]));
   } else {
-    for (size_t i = base; i < n; ++i) dst[i] = (int8_t)(uint8_t)(sm64_mix(state0 + (i + 1) * kGamma) >> 56);
+    for (size_t i = base; i < n; ++i) MIAIE_ST(dst + i, (int8_t)(uint8_t)(sm64_mix(state0 + (i + 1) * kGamma) >> 56));
   }
 }
 
@@ -154,6 +260,18 @@ extern "C" int miaie_init_on_stream(miaie_ctx** out, int device, void* stream) {
     return rc;
   }
   ctx->work_bytes = MIAIE_CTX_WORK_BYTES;
+  // (debug build) the workspace and the scratch array are buffers the
+  // kernels may touch
+  int rc = dbg_add(ctx, ctx->work, ctx->work_bytes);
+  if (rc == MIAIE_OK) rc = dbg_add(ctx, ctx->scratch, MIAIE_MLP_NOALLOC_MAX_H);
+  if (rc != MIAIE_OK) {
+    fail(nullptr, rc, "%s", ctx->err);
+    (void)dbg_remove(ctx, ctx->work);
+    (void)hipFree(ctx->work);
+    (void)hipEventDestroy(ctx->done);
+    delete ctx;
+    return rc;
+  }
   *out = ctx;
   return MIAIE_OK;
 }
@@ -187,7 +305,10 @@ extern "C" int miaie_finish(miaie_ctx* ctx) {
   }
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) rc = MIAIE_EHIP;
-  if (ctx->work) (void)hipFree(ctx->work);
+  if (ctx->work) {
+    (void)dbg_remove(ctx, ctx->work);
+    (void)hipFree(ctx->work);
+  }
   if (ctx->done) (void)hipEventDestroy(ctx->done);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -216,6 +337,11 @@ extern "C" int miaie_alloc(miaie_ctx* ctx, size_t bytes, void** dev_ptr) {
   if (bytes == 0) return fail(ctx, MIAIE_EINVAL, "miaie_alloc: zero bytes");
   hipError_t e = hipMalloc(dev_ptr, bytes);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc");
+  if ((rc = dbg_add(ctx, *dev_ptr, bytes))) {
+    (void)hipFree(*dev_ptr);
+    *dev_ptr = nullptr;
+    return rc;
+  }
   return MIAIE_OK;
 }
 
@@ -224,6 +350,7 @@ extern "C" int miaie_free(miaie_ctx* ctx, void* dev_ptr) {
   if (rc) return rc;
   if ((rc = refuse_while_recording(ctx, "miaie_free"))) return rc;
   if (!dev_ptr) return MIAIE_OK;
+  if ((rc = dbg_remove(ctx, dev_ptr))) return rc;
   hipError_t e = hipFree(dev_ptr);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");
   return MIAIE_OK;
@@ -289,13 +416,13 @@ extern "C" int miaie_wait(miaie_ctx* ctx, int timeout_ms) {
   if (timeout_ms < 0) {
     e = hipEventSynchronize(ctx->done);
     if (e != hipSuccess) return hip_fail(ctx, e, "hipEventSynchronize");
-    return MIAIE_OK;
+    return dbg_take_faults(ctx);
   }
   timespec t0;
   clock_gettime(CLOCK_MONOTONIC, &t0);
   for (;;) {
     e = hipEventQuery(ctx->done);
-    if (e == hipSuccess) return MIAIE_OK;
+    if (e == hipSuccess) return dbg_take_faults(ctx);
     if (e != hipErrorNotReady) return hip_fail(ctx, e, "hipEventQuery");
     timespec t1;
     clock_gettime(CLOCK_MONOTONIC, &t1);
@@ -309,6 +436,26 @@ extern "C" int miaie_wait(miaie_ctx* ctx, int timeout_ms) {
       nanosleep(&nap, nullptr);
     }
   }
+}
+
+// ---------------------------------------------------------------- device bounds checks
+extern "C" int miaie_debug_device_checks(void) { return MIAIE_DEVICE_CHECKS ? 1 : 0; }
+
+extern "C" int miaie_debug_register(miaie_ctx* ctx, const void* dev_ptr, size_t bytes) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if ((rc = refuse_while_recording(ctx, "miaie_debug_register"))) return rc;
+  MIAIE_CHECK_NOT_NULL(ctx, dev_ptr);
+  if (bytes == 0) return fail(ctx, MIAIE_EINVAL, "miaie_debug_register: zero bytes");
+  return dbg_add(ctx, dev_ptr, bytes);
+}
+
+extern "C" int miaie_debug_unregister(miaie_ctx* ctx, const void* dev_ptr) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if ((rc = refuse_while_recording(ctx, "miaie_debug_unregister"))) return rc;
+  MIAIE_CHECK_NOT_NULL(ctx, dev_ptr);
+  return dbg_remove(ctx, dev_ptr);
 }
 
 // ---------------------------------------------------------------- synthetic data

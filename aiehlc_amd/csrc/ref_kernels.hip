@@ -30,15 +30,15 @@ __global__ __launch_bounds__(256) void mm_window_i32(const int32_t* __restrict__
   uint32_t acc = 0;
   for (int k0 = 0; k0 < n; k0 += WT) {
     const int ar = blockIdx.y * WT + ty, ak = k0 + tx;
-    as[ty][tx] = (ar < n && ak < n) ? (uint32_t)A[(size_t)ar * n + ak] : 0u;
+    as[ty][tx] = (ar < n && ak < n) ? (uint32_t)MIAIE_LD(A + (size_t)ar * n + ak) : 0u;
     const int br = blockIdx.x * WT + ty;
-    bs[ty][tx] = (br < n && ak < n) ? (uint32_t)Bt[(size_t)br * n + ak] : 0u;
+    bs[ty][tx] = (br < n && ak < n) ? (uint32_t)MIAIE_LD(Bt + (size_t)br * n + ak) : 0u;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < WT; ++k) acc += as[ty][k] * bs[tx][k];
     __syncthreads();
   }
-  if (i < n && j < n) out[(size_t)i * n + j] = (int32_t)acc;
+  if (i < n && j < n) MIAIE_ST(out + (size_t)i * n + j, (int32_t)acc);
 }
 
 // ---------------------------------------------------------------- dot probe
@@ -53,20 +53,20 @@ __device__ __forceinline__ uint32_t probe_vec2(uint32_t p) { return (0u + (p & 1
 
 __global__ void dot_probe_init(const uint32_t* __restrict__ in, uint32_t* __restrict__ out) {
   if (threadIdx.x != 0) return;
-  const uint32_t p = in[0];
+  const uint32_t p = MIAIE_LD(in);
   const uint64_t reps = 3ull * p;
   uint32_t dot = 0;
   for (uint32_t j = 0; j < 128; ++j) dot += probe_vec1(j, p) * probe_vec2(p);
   const uint32_t rem = (uint32_t)(reps % 1024u);
-  out[0] = (uint32_t)reps;
-  out[1] = 4567u;
-  out[2] = rem * dot;  // the MFMA kernel adds the whole groups
-  out[3] = 3u;
-  out[4] = probe_vec1(0, p);
+  MIAIE_ST(out + 0, (uint32_t)reps);
+  MIAIE_ST(out + 1, 4567u);
+  MIAIE_ST(out + 2, rem * dot);  // the MFMA kernel adds the whole groups
+  MIAIE_ST(out + 3, 3u);
+  MIAIE_ST(out + 4, probe_vec1(0, p));
 }
 
 __global__ __launch_bounds__(256) void dot_probe_mfma(const uint32_t* __restrict__ in, uint32_t* __restrict__ out) {
-  const uint32_t p = in[0];
+  const uint32_t p = MIAIE_LD(in);
   const uint64_t groups = (3ull * p) / 1024u;
   const int lane = threadIdx.x & 63;
   const uint64_t wave_id = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void dot_probe_mfma(const uint32_t* __restrict
   for (int e = 0; e < 16; ++e) s += (uint32_t)acc[e];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-  if (lane == 0 && s) atomicAdd(out + 2, s);
+  if (lane == 0 && s && MIAIE_CHECK(out + 2, sizeof(uint32_t), 1)) atomicAdd(out + 2, s);
 }
 
 // ---------------------------------------------------------------- 3x3 NN, replicated
@@ -110,11 +110,11 @@ __global__ __launch_bounds__(256) void mm_square_u64(const uint64_t* __restrict_
     for (int e = threadIdx.x; e < n * n; e += blockDim.x) {
       const int i = e / n, j = e - i * n;
       uint32_t sum = 0;  // the reference's `int sum`
-      for (int k = 0; k < n; ++k) sum += (uint32_t)(a[i * n + k] * a[k * n + j]);
-      o[e] = (uint64_t)(int64_t)(int32_t)sum;
+      for (int k = 0; k < n; ++k) sum += (uint32_t)(MIAIE_LD(a + i * n + k) * MIAIE_LD(a + k * n + j));
+      MIAIE_ST(o + e, (uint64_t)(int64_t)(int32_t)sum);
     }
     __syncthreads();
-    if (threadIdx.x == 0) o[n * n] = it + 1;
+    if (threadIdx.x == 0) MIAIE_ST(o + n * n, it + 1);
   }
 }
 
@@ -127,9 +127,9 @@ __global__ __launch_bounds__(256) void chain_add_i32(const int32_t* __restrict__
                                                      int len, ChainArgs args, int nstages) {
   // every stage writes out[i] = in[0] + addend for all i, and the next stage
   // reads element 0 of that output
-  uint32_t v = (uint32_t)in[0];
+  uint32_t v = (uint32_t)MIAIE_LD(in);
   for (int s = 0; s < nstages; ++s) v += (uint32_t)args.add[s];
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < len; i += gridDim.x * blockDim.x) out[i] = (int32_t)v;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < len; i += gridDim.x * blockDim.x) MIAIE_ST(out + i, (int32_t)v);
 }
 
 }  // namespace

@@ -37,6 +37,7 @@ extern "C" {
 #define MIAIE_ETIMEDOUT (-3)    /* miaie_wait deadline passed before the stream drained */
 #define MIAIE_ENOMEM (-4)       /* device allocation failed */
 #define MIAIE_EUNSUPPORTED (-5) /* valid request this build does not implement */
+#define MIAIE_EFAULT (-6)       /* debug build: a kernel access outside every known buffer (miaie_wait) */
 
 /* B operand layout of the int8 GEMM.  NT is the reference golden's layout:
  * B stored as [N][K] ("column major", aieml_mm.cc:210-215).  NN is the
@@ -93,6 +94,30 @@ MIAIE_API int miaie_copy_d2d(miaie_ctx* ctx, void* dst_dev, const void* src_dev,
  * context has finished, MIAIE_ETIMEDOUT if timeout_ms elapses first
  * (timeout_ms < 0 waits without a deadline). */
 MIAIE_API int miaie_wait(miaie_ctx* ctx, int timeout_ms);
+
+/* ---- device bounds checks (debug build) --------------------------------- */
+
+/* No counterpart in the reference, whose kernels run unchecked on the AIE
+ * tiles.  The debug build of this library (aiehlc_amd/lib_dbg/, built with
+ * MIAIE_DEVICE_CHECKS=1) checks every global load, store and global->LDS copy
+ * of its kernels against a table of known buffers: every live miaie_alloc
+ * allocation, the context's workspace, the allocation-free entry points'
+ * scratch array, and whatever the caller declares here.  An access that no
+ * buffer contains is not performed (a load reads zeros, a store or copy is
+ * dropped) and is counted; miaie_wait then returns MIAIE_EFAULT, and
+ * miaie_last_error_string names the first such access (load/store/copy,
+ * bytes, address, source file and line).  The product build checks nothing:
+ * miaie_debug_device_checks returns 0 there and the two calls below only
+ * validate their arguments.  Changing the table waits for the whole device
+ * to go idle. */
+MIAIE_API int miaie_debug_device_checks(void);
+/* Declare [dev_ptr, dev_ptr + bytes) as a buffer kernels may touch (memory
+ * not from miaie_alloc), or give a known buffer (same dev_ptr) a new extent,
+ * e.g. a smaller one to check that a kernel stays inside it.  A range that
+ * overlaps another known buffer is refused with MIAIE_EINVAL. */
+MIAIE_API int miaie_debug_register(miaie_ctx* ctx, const void* dev_ptr, size_t bytes);
+/* Forget the buffer that starts at dev_ptr (miaie_free does this itself). */
+MIAIE_API int miaie_debug_unregister(miaie_ctx* ctx, const void* dev_ptr);
 
 /* ---- GEMM planning ------------------------------------------------------ */
 

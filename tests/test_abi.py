@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -62,7 +63,8 @@ def test_null_context_is_rejected():
 
 def test_status_codes_match_header():
     text = open(mi.HEADER_PATH).read()
-    for name in ("MIAIE_OK", "MIAIE_EINVAL", "MIAIE_EHIP", "MIAIE_ETIMEDOUT", "MIAIE_ENOMEM", "MIAIE_EUNSUPPORTED"):
+    for name in ("MIAIE_OK", "MIAIE_EINVAL", "MIAIE_EHIP", "MIAIE_ETIMEDOUT", "MIAIE_ENOMEM", "MIAIE_EUNSUPPORTED",
+                 "MIAIE_EFAULT"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m and int(m.group(1)) == getattr(mi, name), name
     # the conv planner's kernel ids, as the Python binding names them
@@ -113,3 +115,18 @@ def test_conv_planner_keeps_32_bit_offsets_in_range():
     assert mi.plan_conv2d_i8(1, 1, 1, 256, big_deep + 64 - big_deep % 64) == "igemm"
     with pytest.raises(mi.MiaieError):
         mi.plan_conv2d_i8(1, 2, 2, 4, 4, 5, 5, 1, 0)                  # filter larger than the input
+
+
+def test_device_checked_build_exports_the_same_boundary():
+    """aiehlc_amd/lib_dbg/libmiaie.so (device-side bounds checks) exports
+    exactly the header's entry points and says it checks; the product build
+    says it does not.  The debug build is loaded in a process of its own."""
+    dbg = os.path.join(ROOT, "aiehlc_amd", "lib_dbg", "libmiaie.so")
+    if not os.path.exists(dbg):
+        pytest.skip("device-checked build missing")
+    exported = {s for s in _exported(dbg) if s.startswith("miaie_")}
+    assert exported == set(mi.header_functions()), exported ^ set(mi.header_functions())
+    assert mi.load_library().miaie_debug_device_checks() == 0
+    code = f"import ctypes; print(ctypes.CDLL({dbg!r}).miaie_debug_device_checks())"
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True).stdout
+    assert out.strip() == "1"
