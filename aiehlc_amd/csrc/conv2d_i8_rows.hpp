@@ -147,7 +147,7 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
     t0 = __builtin_amdgcn_s_memtime();
     r0 = __builtin_amdgcn_s_memrealtime();
   }
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fh = lane >> 5;
   int n, rb, cb;
   if (xg) {
@@ -175,11 +175,22 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   // wave: output row rr, pixels 32pb .. +32, channels 32wc .. +32
   const int wc = wave % G::NWC, pb = (wave / G::NWC) & 1, rr = wave / (2 * G::NWC);
 
-  // this lane's 16 output channels' shifts (4 per dword), loaded up front so
-  // their latency hides under the staging
-  uint32_t sh4[4];
+  // the wave's 32 output channels' shifts (4 per dword): one wave-uniform
+  // load through the scalar cache, so the staging below is the only
+  // vector-memory work ahead of the first wait (four per-lane loads of them
+  // measured 1-2% slower per launch: the staging is bound by the issue of its
+  // load instructions, not by their bytes)
+  uint32_t s8[8];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) sh4[g] = MIAIE_LD(reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc + 8 * g + 4 * fh));
+  for (int q = 0; q < 8; ++q) s8[q] = MIAIE_LD(reinterpret_cast<const uint32_t*>(shifts + co0 + 32 * wc) + q);
+  // a wave-uniform value the compiler cannot see through: the conditional
+  // last W pass below stays a branch around its load and its LDS write
+  // instead of being merged into one block with a wait for the load
+  auto opaque = [](int v) {
+    asm volatile("" : "+s"(v));
+    return v;
+  };
+  constexpr int WRW = (G::WREM + 63) / 64;  // waves that have chunks in the last W pass
 
   // ---- stage X (zero outside the image) and W.  Every load is issued before
   // any is waited for: positions outside the image load the nearest chunk
@@ -207,12 +218,26 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
   for (int u = 0; u < G::XQ; ++u)
     xv[u] = MIAIE_LD(reinterpret_cast<const v4i*>(X + x_off(xrow_of(u), xcol, xc, xin[u])));
   xe = MIAIE_LD(reinterpret_cast<const v4i*>(X + x_off(erow, ecol, ec, ein)));
-  // (threads past the end of the last W pass repeat that pass's chunks)
+  // (the last W pass is issued by the WRW waves that have chunks in it; the
+  // lanes of a partial wave past its end repeat that pass's chunks)
   auto wq_of = [&](int u) { return u < G::WQ - 1 ? tid + 512 * u : 512 * (G::WQ - 1) + tid % G::WREM; };
 #pragma unroll
-  for (int u = 0; u < G::WQ; ++u) wv[u] = MIAIE_LD(reinterpret_cast<const v4i*>(W + (uint32_t)(co0 * G::RSC + 16 * wq_of(u))));
+  for (int u = 0; u < G::WQ - 1; ++u)
+    wv[u] = MIAIE_LD(reinterpret_cast<const v4i*>(W + (uint32_t)(co0 * G::RSC + 16 * wq_of(u))));
+  if (opaque(wave) < WRW)
+    wv[G::WQ - 1] = MIAIE_LD(reinterpret_cast<const v4i*>(W + (uint32_t)(co0 * G::RSC + 16 * wq_of(G::WQ - 1))));
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
 
+  // This lane's 16 channels' shifts: channels 32wc + 8g + 4fh + tt.  (The
+  // values pass through an empty asm so that the select stays a select of
+  // two registers and does not become a lane-indexed read of s8.)
+  uint32_t sh4[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    uint32_t lo = s8[2 * g], hi = s8[2 * g + 1];
+    asm("" : "+s"(lo), "+s"(hi));
+    sh4[g] = fh ? hi : lo;
+  }
   // The accumulators start at the rounding term 2^(s-1) of their channel
   // (|acc| <= R*S*CIN * 2^14 < 2^30 keeps acc + 2^30 inside int32), so the
   // epilogue only shifts and saturates.  Computed here, while the staging
@@ -236,11 +261,12 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
 #pragma unroll
   for (int u = 0; u < G::XQ; ++u) x_put(xrow_of(u), xcol, xc, xin[u], xv[u]);
   x_put(erow, ecol, ec, ein, xe);
+  auto w_put = [&](int q, v4i v) {
+    *reinterpret_cast<v4i*>(ws + (q / (G::RSC / 16)) * G::WP + 16 * (q % (G::RSC / 16))) = v;
+  };
 #pragma unroll
-  for (int u = 0; u < G::WQ; ++u) {
-    const int q = wq_of(u);
-    *reinterpret_cast<v4i*>(ws + (q / (G::RSC / 16)) * G::WP + 16 * (q % (G::RSC / 16))) = wv[u];
-  }
+  for (int u = 0; u < G::WQ - 1; ++u) w_put(wq_of(u), wv[u]);
+  if (opaque(wave) < WRW) w_put(wq_of(G::WQ - 1), wv[G::WQ - 1]);
   __syncthreads();
   unsigned long long t1 = 0;
   if constexpr (TIMED) t1 = __builtin_amdgcn_s_memtime();
@@ -275,14 +301,15 @@ __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__
 // Grid and launch of the row-block kernel (shapes already checked by the
 // caller: rows_ok in conv2d_kernel_for).
 template <int CIN, int ROWS, int WCO, bool TIMED>
-inline void launch_rows_as(hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
-                           int H, int Wd, int Cout, int pad, int Ho, int Wo, unsigned long long* probe = nullptr) {
+inline hipError_t launch_rows_as(int device, hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts,
+                                 int8_t* Y, int N, int H, int Wd, int Cout, int pad, int Ho, int Wo,
+                                 unsigned long long* probe = nullptr) {
   const int ncb = (Wo + PB - 1) / PB;
   const unsigned rbs = (unsigned)((Ho + ROWS - 1) / ROWS * ncb), cbs = (unsigned)(Cout / WCO);
   const bool by_xcd = N % 8 == 0 && rbs <= 65535 && (size_t)(N / 8) * cbs <= 65535;
   const dim3 grid = by_xcd ? dim3(8, rbs, (unsigned)(N / 8) * cbs) : dim3(rbs, cbs, (unsigned)N);
-  hipLaunchKernelGGL((conv2d_i8_rows<3, 3, CIN, ROWS, WCO, TIMED>), grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd,
-                     Cout, pad, Ho, Wo, by_xcd ? N / 8 : 0, ncb, probe);
+  return launch<conv2d_i8_rows<3, 3, CIN, ROWS, WCO, TIMED>>(device, grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd,
+                                                             Cout, pad, Ho, Wo, by_xcd ? N / 8 : 0, ncb, probe);
 }
 
 
@@ -475,14 +502,14 @@ __global__ __launch_bounds__(512) void conv2d_i8_rowsk(const int8_t* __restrict_
 // Grid and launch of the chunked row-block kernel (shapes already checked by
 // the caller: deep_ok in conv2d_kernel_for).
 template <int ROWS, int WCO, int NJ, int BW>
-inline void launch_rowsk_as(hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts, int8_t* Y, int N,
-                            int H, int Wd, int Cin, int Cout, int pad, int Ho, int Wo) {
+inline hipError_t launch_rowsk_as(int device, hipStream_t st, const int8_t* X, const int8_t* W, const uint8_t* shifts,
+                                  int8_t* Y, int N, int H, int Wd, int Cin, int Cout, int pad, int Ho, int Wo) {
   const int ncb = (Wo + BW - 1) / BW;
   const unsigned rbs = (unsigned)((Ho + ROWS - 1) / ROWS * ncb), cbs = (unsigned)(Cout / WCO);
   const bool by_xcd = N % 8 == 0 && rbs <= 65535 && (size_t)(N / 8) * cbs <= 65535;
   const dim3 grid = by_xcd ? dim3(8, rbs, (unsigned)(N / 8) * cbs) : dim3(rbs, cbs, (unsigned)N);
-  hipLaunchKernelGGL((conv2d_i8_rowsk<ROWS, WCO, NJ, BW>), grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd, Cin, Cout, pad, Ho,
-                     Wo, by_xcd ? N / 8 : 0, ncb);
+  return launch<conv2d_i8_rowsk<ROWS, WCO, NJ, BW>>(device, grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd, Cin, Cout,
+                                                    pad, Ho, Wo, by_xcd ? N / 8 : 0, ncb);
 }
 
 

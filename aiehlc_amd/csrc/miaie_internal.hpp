@@ -3,9 +3,12 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <tuple>
+#include <utility>
 
 #include "../../include/miaie.h"
 #include "dbg_checks.hpp"
@@ -36,6 +39,51 @@ int fail(miaie_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(p
 
 // Map a HIP error to MIAIE_EHIP with a message naming the call.
 int hip_fail(miaie_ctx* ctx, hipError_t e, const char* what);
+
+// Check a launch's result (MIAIE_EHIP naming the kernel when it failed).
+int check_launch(miaie_ctx* ctx, hipError_t e, const char* kernel);
+
+template <class F>
+struct kernel_sig;
+template <class... P>
+struct kernel_sig<void (*)(P...)> {
+  using args = std::tuple<P...>;
+};
+
+// Launch kernel K through the module API, with its handle looked up once per
+// device (device < 0: the current one, read on every call).  hipLaunchKernel
+// finds the kernel from its host address on every call and reports a failed
+// launch through a second call, hipGetLastError: on the host, 2.95 us per
+// launch against 2.81 us here, measured with an empty kernel of the conv's
+// 13 arguments.  The arguments are first converted to the kernel's parameter
+// types, since the runtime copies each by the size of its parameter.  The
+// caller has the device current (hipGetFuncBySymbol resolves on it).
+constexpr int kLaunchCacheDevices = 64;
+template <auto K, class... A>
+hipError_t launch(int device, dim3 grid, dim3 block, size_t lds_bytes, hipStream_t st, A&&... a) {
+  using Args = typename kernel_sig<decltype(K)>::args;
+  static_assert(std::tuple_size<Args>::value == sizeof...(A) && sizeof...(A) > 0, "kernel argument count");
+  static std::atomic<hipFunction_t> cache[kLaunchCacheDevices];
+  if (device < 0) {
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+  }
+  const bool cached = device < kLaunchCacheDevices;
+  hipFunction_t f = cached ? cache[device].load(std::memory_order_acquire) : nullptr;
+  if (!f) {
+    hipError_t e = hipGetFuncBySymbol(&f, reinterpret_cast<const void*>(K));
+    if (e != hipSuccess) return e;
+    if (cached) cache[device].store(f, std::memory_order_release);
+  }
+  Args vals(std::forward<A>(a)...);
+  void* ptrs[sizeof...(A)];
+  std::apply([&](auto&... v) {
+    int i = 0;
+    ((ptrs[i++] = static_cast<void*>(&v)), ...);
+  }, vals);
+  return hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, (unsigned)lds_bytes, st, ptrs,
+                               nullptr);
+}
 
 // Every entry point starts with this: non-null context, its device current.
 int enter(miaie_ctx* ctx);

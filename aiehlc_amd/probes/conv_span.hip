@@ -43,7 +43,7 @@
 
 namespace {
 
-constexpr int N = 8, H = 56, Wd = 56, CIN = 64, COUT = 64, ROWS = 2, WCO = 64;
+constexpr int N = 8, H = 56, Wd = 56, CIN = 64, COUT = 64, ROWS = 4, WCO = 32;
 
 uint64_t mix(uint64_t z) {
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -75,7 +75,7 @@ int main(int argc, char** argv) {
   for (size_t i = 0; i < xb; ++i) hx[i] = (int8_t)(mix(0x1000 + i) >> 56);
   for (size_t i = 0; i < wb; ++i) hw[i] = (int8_t)(mix(0x2000000 + i) >> 56);
   for (int i = 0; i < COUT; ++i) hs[i] = (uint8_t)(8 + mix(0x3000000 + i) % 5);
-  const int waves = 8 * (H / ROWS) * N;  // 224 workgroups of 8 waves
+  const int waves = 8 * (H / ROWS) * (COUT / WCO) * N;  // 224 workgroups of 8 waves
   int8_t *X, *W, *Y;
   uint8_t* S;
   unsigned long long* P;
@@ -90,10 +90,10 @@ int main(int argc, char** argv) {
   hipStream_t st;
   CHECK(hipStreamCreate(&st));
   auto product = [&]() {
-    miaie::conv::launch_rows_as<CIN, ROWS, WCO, false>(st, X, W, S, Y, N, H, Wd, COUT, 1, H, Wd);
+    CHECK(miaie::conv::launch_rows_as<CIN, ROWS, WCO, false>(0, st, X, W, S, Y, N, H, Wd, COUT, 1, H, Wd));
   };
   auto timed = [&]() {
-    miaie::conv::launch_rows_as<CIN, ROWS, WCO, true>(st, X, W, S, Y, N, H, Wd, COUT, 1, H, Wd, P);
+    CHECK(miaie::conv::launch_rows_as<CIN, ROWS, WCO, true>(0, st, X, W, S, Y, N, H, Wd, COUT, 1, H, Wd, P));
   };
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
@@ -158,7 +158,7 @@ int main(int argc, char** argv) {
     ghz += (double)(p[3] - p[0]) / ((double)(p[5] - p[4]) * 10.0) / waves;
   }
   const double span_us = (double)(wall1 - wall0) / 100.0;
-  printf("{\"kernel\": \"conv2d_i8_rows<3, 3, 64, 2, 64>\", \"config\": \"N=8 56x56 Cin=Cout=64 3x3 pad 1\", "
+  printf("{\"kernel\": \"conv2d_i8_rows<3, 3, 64, 4, 32>\", \"config\": \"N=8 56x56 Cin=Cout=64 3x3 pad 1\", "
          "\"timed_output_equals_product\": %s, \"span_us\": %.3f, \"last_start_us\": %.3f, "
          "\"staging_cycles\": [%.0f, %.0f], \"mfma_cycles\": [%.0f, %.0f], \"epilogue_cycles\": [%.0f, %.0f], "
          "\"clock_ghz\": %.3f, \"us_per_launch_product\": %.3f, \"us_per_launch_timed\": %.3f, \"launches\": %d, "

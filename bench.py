@@ -428,7 +428,7 @@ def extra_conv(ctx, timer, args) -> dict:
             span["device_frac"] = round(conv_ops / (span["device_us"] * 1e-6) / 1e12 / roof, 4)
     return {
         "config": "N=8 H=W=56 Cin=Cout=64 3x3 stride 1 pad 1, NHWC x OHWI, per-channel shift in [8,12]",
-        "kernel": "conv2d_i8_rows<3,3,64,2,64> (2 output rows x 64 channels per workgroup, image-per-XCD grid)",
+        "kernel": "conv2d_i8_rows<3,3,64,4,32> (4 output rows x 32 channels per workgroup, image-per-XCD grid)",
         "us_per_step": round(us_c, 3),
         "us_per_step_from": step_from,
         "gops": round(conv_ops / (us_c * 1e-6) / 1e9, 1),

@@ -299,15 +299,17 @@ CONV_SHAPES = [
     (1, 9, 9, 32, 64, 5, 5, 1, 2),
     (1, 7, 64, 64, 128, 3, 3, 1, 1),  # odd Ho, Wo = 64, two Cout blocks
     (3, 5, 33, 32, 64, 3, 3, 1, 0),   # no padding
-    (2, 56, 56, 64, 64, 3, 3, 1, 1),  # config shape, fewer images
-    (1, 5, 48, 64, 64, 3, 3, 1, 1),   # row-pair kernel: odd Ho (last workgroup half outside the image)
+    (2, 56, 56, 64, 64, 3, 3, 1, 1),  # config shape, fewer images (row-block 4 rows x 32 channels)
+    (1, 5, 48, 64, 64, 3, 3, 1, 1),   # row-pair (2 x 64, Ho < 8): odd Ho (last workgroup half outside the image)
     (2, 6, 50, 64, 128, 3, 3, 1, 0),  # row-pair, no padding, two Cout blocks
-    (1, 9, 60, 64, 64, 3, 3, 1, 2),   # row-pair, pad 2 (two zero columns each side)
+    (1, 9, 60, 64, 64, 3, 3, 1, 2),   # row-block 4 x 32, pad 2 (two zero columns each side), Ho 11: last block 3 rows
     (1, 4, 64, 64, 64, 3, 3, 1, 0),   # row-pair, widest row, no padding
     (1, 7, 56, 64, 32, 3, 3, 1, 1),   # row-block 4 rows x 32 channels (Cout 32), last block half outside
     (2, 5, 30, 32, 96, 3, 3, 1, 1),   # row-block 4 x 32, three channel blocks, Cin 32
     (2, 7, 28, 128, 128, 3, 3, 1, 1),  # row-block 2 x 64 at Cin 128 (108 KiB of LDS), odd Ho
     (1, 6, 60, 128, 96, 3, 3, 1, 2),  # row-block 4 x 32 at Cin 128, pad 2
+    (1, 10, 64, 128, 128, 3, 3, 1, 1),  # row-block 4 x 32 at Cin 128, four channel blocks, last block half outside
+    (2, 11, 40, 32, 64, 3, 3, 1, 1),  # row-block 4 x 32 at Cin 32, Cout 64, last block 3 rows
     (1, 5, 9, 96, 64, 3, 3, 1, 1),    # Cin 96: implicit-GEMM kernel
     (1, 8, 8, 256, 64, 3, 3, 1, 1),   # chunked row-block kernel: four 64-channel chunks, one workgroup
     (1, 16, 16, 256, 64, 3, 3, 2, 1),  # taps kernel (LDS-staged), stride 2: one tile split 4 ways over k (partials + reduce)
