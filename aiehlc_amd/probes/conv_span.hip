@@ -90,10 +90,10 @@ int main(int argc, char** argv) {
   hipStream_t st;
   CHECK(hipStreamCreate(&st));
   auto product = [&]() {
-    CHECK(miaie::conv::launch_rows_as<CIN, ROWS, WCO, false>(0, st, X, W, S, Y, N, H, Wd, COUT, 1, H, Wd));
+    CHECK((miaie::conv::launch_rows_as<CIN, ROWS, WCO, false>(0, st, X, W, S, Y, N, H, Wd, COUT, 1, H, Wd)));
   };
   auto timed = [&]() {
-    CHECK(miaie::conv::launch_rows_as<CIN, ROWS, WCO, true>(0, st, X, W, S, Y, N, H, Wd, COUT, 1, H, Wd, P));
+    CHECK((miaie::conv::launch_rows_as<CIN, ROWS, WCO, true>(0, st, X, W, S, Y, N, H, Wd, COUT, 1, H, Wd, P)));
   };
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));

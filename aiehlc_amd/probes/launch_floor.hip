@@ -107,8 +107,8 @@ int main(int argc, char** argv) {
   CHECK(hipStreamCreate(&st));
   CHECK(hipMalloc(&out, 4096 * sizeof(int)));
   printf("{\n");
-  // conv2d_i8_rows<3,3,64,2,64> at N=8, 56x56: 224 workgroups (8 x 28 x 1) of 512 threads, 65024 B of LDS
-  run<65024, 512>(st, out, 224, iters, "conv2d_rows_grid", false);
+  // conv2d_i8_rows<3,3,64,4,32> at N=8, 56x56: 224 workgroups (8 x 14 x 2) of 512 threads, 56576 B of LDS
+  run<56576, 512>(st, out, 224, iters, "conv2d_rows_grid", false);
   // gemm_i8_pipe16<256,256> at 4096^3: 256 workgroups of 256 threads, 160 KiB of LDS
   run<163840, 256>(st, out, 256, iters, "gemm_256x256_grid", false);
   run<0, 64>(st, out, 1, iters, "one_wave", true);
