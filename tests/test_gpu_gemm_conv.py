@@ -455,8 +455,9 @@ def test_conv2d_i8_rows_deep(ctx, shape, cus, extreme):
 
 
 @pytest.mark.parametrize("shape", [
-    (1, 6, 56, 64, 64, 3, 3, 1, 1),   # row-block 2 rows x 64 channels
-    (1, 5, 20, 32, 96, 3, 3, 1, 1),   # row-block 4 rows x 32 channels
+    (1, 6, 56, 64, 64, 3, 3, 1, 1),   # row-block 2 rows x 64 channels (Ho < 8)
+    (1, 9, 56, 64, 64, 3, 3, 1, 1),   # row-block 4 rows x 32 channels, two channel blocks (config 4's workgroup)
+    (1, 5, 20, 32, 96, 3, 3, 1, 1),   # row-block 4 rows x 32 channels, three channel blocks
     (1, 4, 24, 128, 64, 3, 3, 1, 1),  # row-block at Cin 128
     (1, 8, 8, 64, 64, 3, 3, 2, 1),    # implicit-GEMM kernel
     (1, 16, 16, 256, 64, 3, 3, 2, 1),  # taps kernel split over k (requantize in the reduce kernel)
