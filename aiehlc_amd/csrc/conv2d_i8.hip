@@ -531,8 +531,9 @@ static RowsDeepTile rows_deep_tile(int N, int Ho, int Wo, int Cin, int Cout, int
   return best;
 }
 
-// conv2d_i8_rows<3,3,128,...> (118 KiB of LDS: one workgroup per CU), 3.57
-// us per workgroup (8x112x112x128 in 7 rounds, 25.0 us)
+// conv2d_i8_rows<3,3,128,...> (98 KiB of LDS at 4 rows x 32 channels, 116 KiB
+// at 2 x 64: one workgroup per CU), 3.5-3.6 us per workgroup (8x112x112x128
+// in 7 rounds, 24.4-25.1 us)
 static double rows128_us(int N, int Ho, int Wo, int Cout, int cus) {
   const int rows = rows_tall(Ho, Cout) ? 4 : 2, wco = rows_tall(Ho, Cout) ? 32 : 64;
   const size_t wgs = (size_t)N * ((Ho + rows - 1) / rows) * ((Wo + conv::PB - 1) / conv::PB) * (size_t)(Cout / wco);

@@ -306,7 +306,7 @@ CONV_SHAPES = [
     (1, 4, 64, 64, 64, 3, 3, 1, 0),   # row-pair, widest row, no padding
     (1, 7, 56, 64, 32, 3, 3, 1, 1),   # row-block 4 rows x 32 channels (Cout 32), last block half outside
     (2, 5, 30, 32, 96, 3, 3, 1, 1),   # row-block 4 x 32, three channel blocks, Cin 32
-    (2, 7, 28, 128, 128, 3, 3, 1, 1),  # row-block 2 x 64 at Cin 128 (108 KiB of LDS), odd Ho
+    (2, 7, 28, 128, 128, 3, 3, 1, 1),  # row-block 2 x 64 at Cin 128 (116 KiB of LDS), Ho < 8 and odd
     (1, 6, 60, 128, 96, 3, 3, 1, 2),  # row-block 4 x 32 at Cin 128, pad 2
     (1, 10, 64, 128, 128, 3, 3, 1, 1),  # row-block 4 x 32 at Cin 128, four channel blocks, last block half outside
     (2, 11, 40, 32, 64, 3, 3, 1, 1),  # row-block 4 x 32 at Cin 32, Cout 64, last block 3 rows
