@@ -683,21 +683,21 @@ int launch_gemm_bf16(miaie_ctx* ctx, const uint16_t* A, const uint16_t* B, float
   const bool big = (whole || overlap) && K % BK == 0 && aligned(A, 16) && aligned(B, 16) && aligned(C, 16) &&
                    K < (1 << 24) && N < (1 << 24);
   if (big && K % (2 * BK) == 0) {
-    hipLaunchKernelGGL(gemm_bf16_pair16, dim3(tiles), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
-    return check_launch(ctx, "gemm_bf16_pair16");
+    return check_launch(ctx, launch<gemm_bf16_pair16>(ctx->device, dim3(tiles), dim3(256), 0, ctx->stream, A, B, C, M, N, K),
+                        "gemm_bf16_pair16");
   }
   if (big) {
-    hipLaunchKernelGGL(gemm_bf16_tile256, dim3(tiles), dim3(256), 0, ctx->stream, A, B, C, M, N, K);
-    return check_launch(ctx, "gemm_bf16_tile256");
+    return check_launch(ctx, launch<gemm_bf16_tile256>(ctx->device, dim3(tiles), dim3(256), 0, ctx->stream, A, B, C, M, N, K),
+                        "gemm_bf16_tile256");
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64);
   if (grid.y > 65535) return fail(ctx, MIAIE_EINVAL, "gemm_bf16: M too large for the 64x64 fallback");
   if (K % 8 == 0 && aligned(A, 16)) {
-    hipLaunchKernelGGL(gemm_bf16_tile64p, grid, dim3(256), 0, ctx->stream, A, B, C, M, N, K);
-    return check_launch(ctx, "gemm_bf16_tile64p");
+    return check_launch(ctx, launch<gemm_bf16_tile64p>(ctx->device, grid, dim3(256), 0, ctx->stream, A, B, C, M, N, K),
+                        "gemm_bf16_tile64p");
   }
-  hipLaunchKernelGGL(gemm_bf16_tile64, grid, dim3(256), 0, ctx->stream, A, B, C, M, N, K);
-  return check_launch(ctx, "gemm_bf16_tile64");
+  return check_launch(ctx, launch<gemm_bf16_tile64>(ctx->device, grid, dim3(256), 0, ctx->stream, A, B, C, M, N, K),
+                      "gemm_bf16_tile64");
 }
 
 }  // namespace miaie

@@ -43,6 +43,8 @@ namespace {
 
 namespace dev = miaie::dev;
 using namespace miaie::gemm;
+using miaie::kernel_t;
+using miaie::launch;
 
 // ------------------------------------------------------------ 64x64 tile
 // Bounds-checked fallback for shapes and strides the 256 kernel does not take.
@@ -211,20 +213,21 @@ __global__ __launch_bounds__(256) void gemm_i8_tile64p(const int8_t* __restrict_
 // leave it in the caches (instantiated for NN B with ReLU, the MLP's form;
 // other calls ignore it).
 template <int BM, int BN, bool B_NT>
-void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
-                 int lda, int ldb, int ldy, int ldc, int shift, int relu, bool keep_y) {
+hipError_t launch_pipe(int device, hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M,
+                       int N, int K, int lda, int ldb, int ldy, int ldc, int shift, int relu, bool keep_y) {
   // 128x128 tiles (small grids, where the power limit does not bind): two
   // waves per SIMD, so one wave's MFMAs run while the other waits at the
   // k-tile's barrier or for its LDS reads
   constexpr int NW = BM == 128 ? 8 : 4;
   dim3 grid(((M + BM - 1) / BM) * ((N + BN - 1) / BN)), block(64 * NW);
   const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
-  auto go = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
+  hipError_t e = hipSuccess;
+  auto go = [&](auto k) {
+    e = launch<decltype(k)::value>(device, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu);
   };
-  auto go2 = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu,
-                       (unsigned long long*)nullptr);
+  auto go2 = [&](auto k) {
+    e = launch<decltype(k)::value>(device, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu,
+                                   nullptr);
   };
   // 256-row tiles with K a multiple of 128: A staged two k-tiles at a time,
   // 16x16x64 MFMAs (gemm_i8_pipe16).  128x128 tiles keep gemm_i8_pipe.
@@ -233,76 +236,81 @@ void launch_pipe(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, in
       if constexpr (!B_NT) {
         if (keep_y && Y && !C && relu) {
           if (yq == Y_HI_RELU)
-            go2(gemm_i8_pipe16<BM, BN, NW, false, Y_HI_RELU, false, false, true>);
+            go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, false, Y_HI_RELU, false, false, true>>{});
           else
-            go2(gemm_i8_pipe16<BM, BN, NW, false, Y_MED3, false, false, true>);
-          return;
+            go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, false, Y_MED3, false, false, true>>{});
+          return e;
         }
       }
       if (C) {
         switch (yq) {
-          case Y_NONE: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_NONE, true>); break;
-          case Y_MED3: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_MED3, true>); break;
-          case Y_HI: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI, true>); break;
-          default: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI_RELU, true>); break;
+          case Y_NONE: go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, B_NT, Y_NONE, true>>{}); break;
+          case Y_MED3: go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, B_NT, Y_MED3, true>>{}); break;
+          case Y_HI: go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI, true>>{}); break;
+          default: go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI_RELU, true>>{}); break;
         }
       } else {
         switch (yq) {
-          case Y_MED3: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_MED3, false>); break;
-          case Y_HI: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI, false>); break;
-          default: go2(gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI_RELU, false>); break;
+          case Y_MED3: go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, B_NT, Y_MED3, false>>{}); break;
+          case Y_HI: go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI, false>>{}); break;
+          default: go2(kernel_t<gemm_i8_pipe16<BM, BN, NW, B_NT, Y_HI_RELU, false>>{}); break;
         }
       }
-      return;
+      return e;
     }
   }
   if (C) {
     switch (yq) {
-      case Y_NONE: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_NONE, true>); break;
-      case Y_MED3: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_MED3, true>); break;
-      case Y_HI: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI, true>); break;
-      default: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI_RELU, true>); break;
+      case Y_NONE: go(kernel_t<gemm_i8_pipe<BM, BN, NW, B_NT, Y_NONE, true>>{}); break;
+      case Y_MED3: go(kernel_t<gemm_i8_pipe<BM, BN, NW, B_NT, Y_MED3, true>>{}); break;
+      case Y_HI: go(kernel_t<gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI, true>>{}); break;
+      default: go(kernel_t<gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI_RELU, true>>{}); break;
     }
   } else {
     switch (yq) {
-      case Y_MED3: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_MED3, false>); break;
-      case Y_HI: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI, false>); break;
-      default: go(gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI_RELU, false>); break;
+      case Y_MED3: go(kernel_t<gemm_i8_pipe<BM, BN, NW, B_NT, Y_MED3, false>>{}); break;
+      case Y_HI: go(kernel_t<gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI, false>>{}); break;
+      default: go(kernel_t<gemm_i8_pipe<BM, BN, NW, B_NT, Y_HI_RELU, false>>{}); break;
     }
   }
+  return e;
 }
 
 template <bool B_NT>
-void launch_pipe_mixed(hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C, int M, int N, int K,
-                       int lda, int ldb, int ldy, int ldc, int shift, int relu, int nw, bool keep_y) {
+hipError_t launch_pipe_mixed(int device, hipStream_t st, const int8_t* A, const int8_t* B, int8_t* Y, int32_t* C,
+                             int M, int N, int K, int lda, int ldb, int ldy, int ldc, int shift, int relu, int nw,
+                             bool keep_y) {
   const dim3 grid(((M + 255) / 256) * (nw + (N - 256 * nw + 127) / 128)), block(256);
   const int yq = !Y ? Y_NONE : shift < 8 ? Y_MED3 : relu ? Y_HI_RELU : Y_HI;
-  auto go = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw);
+  hipError_t e = hipSuccess;
+  auto go = [&](auto k) {
+    e = launch<decltype(k)::value>(device, grid, block, 0, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu,
+                                   nw);
   };
   if constexpr (!B_NT) {
     if (keep_y && Y && !C && relu) {
       if (yq == Y_HI_RELU)
-        go(gemm_i8_pipe16_mixed<false, Y_HI_RELU, false, true>);
+        go(kernel_t<gemm_i8_pipe16_mixed<false, Y_HI_RELU, false, true>>{});
       else
-        go(gemm_i8_pipe16_mixed<false, Y_MED3, false, true>);
-      return;
+        go(kernel_t<gemm_i8_pipe16_mixed<false, Y_MED3, false, true>>{});
+      return e;
     }
   }
   if (C) {
     switch (yq) {
-      case Y_NONE: go(gemm_i8_pipe16_mixed<B_NT, Y_NONE, true>); break;
-      case Y_MED3: go(gemm_i8_pipe16_mixed<B_NT, Y_MED3, true>); break;
-      case Y_HI: go(gemm_i8_pipe16_mixed<B_NT, Y_HI, true>); break;
-      default: go(gemm_i8_pipe16_mixed<B_NT, Y_HI_RELU, true>); break;
+      case Y_NONE: go(kernel_t<gemm_i8_pipe16_mixed<B_NT, Y_NONE, true>>{}); break;
+      case Y_MED3: go(kernel_t<gemm_i8_pipe16_mixed<B_NT, Y_MED3, true>>{}); break;
+      case Y_HI: go(kernel_t<gemm_i8_pipe16_mixed<B_NT, Y_HI, true>>{}); break;
+      default: go(kernel_t<gemm_i8_pipe16_mixed<B_NT, Y_HI_RELU, true>>{}); break;
     }
   } else {
     switch (yq) {
-      case Y_MED3: go(gemm_i8_pipe16_mixed<B_NT, Y_MED3, false>); break;
-      case Y_HI: go(gemm_i8_pipe16_mixed<B_NT, Y_HI, false>); break;
-      default: go(gemm_i8_pipe16_mixed<B_NT, Y_HI_RELU, false>); break;
+      case Y_MED3: go(kernel_t<gemm_i8_pipe16_mixed<B_NT, Y_MED3, false>>{}); break;
+      case Y_HI: go(kernel_t<gemm_i8_pipe16_mixed<B_NT, Y_HI, false>>{}); break;
+      default: go(kernel_t<gemm_i8_pipe16_mixed<B_NT, Y_HI_RELU, false>>{}); break;
     }
   }
+  return e;
 }
 
 // Tiling planner for the pipelined kernel: picks the workgroup tile
@@ -448,44 +456,47 @@ int launch_gemm_i8(miaie_ctx* ctx, const int8_t* A, const int8_t* B, int8_t* Y, 
   plan_gemm_i8(ctx, M, N, K, dense_ok, &plan);
   if (plan.kernel == MIAIE_KERNEL_PIPE_MIXED) {
     const int nw = plan_pipe(M, N, K, ctx->cus).nw;
-    b_nt ? launch_pipe_mixed<true>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw, keep_y)
-         : launch_pipe_mixed<false>(ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw, keep_y);
-    return check_launch(ctx, "gemm_i8_pipe16_mixed");
+    const int dev = ctx->device;
+    const hipError_t e =
+        b_nt ? launch_pipe_mixed<true>(dev, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw, keep_y)
+             : launch_pipe_mixed<false>(dev, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, nw,
+                                        keep_y);
+    return check_launch(ctx, e, "gemm_i8_pipe16_mixed");
   }
   if (plan.kernel == MIAIE_KERNEL_PIPE) {
     hipStream_t st = ctx->stream;
-    const int bm = plan.tile_m, bn = plan.tile_n;
+    const int dev = ctx->device, bm = plan.tile_m, bn = plan.tile_n;
+    hipError_t e;
     if (bm == 256 && bn == 256)
-      b_nt ? launch_pipe<256, 256, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
-           : launch_pipe<256, 256, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
+      e = b_nt ? launch_pipe<256, 256, true>(dev, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
+               : launch_pipe<256, 256, false>(dev, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
     else if (bm == 256)
-      b_nt ? launch_pipe<256, 128, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
-           : launch_pipe<256, 128, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
+      e = b_nt ? launch_pipe<256, 128, true>(dev, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
+               : launch_pipe<256, 128, false>(dev, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
     else
-      b_nt ? launch_pipe<128, 128, true>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
-           : launch_pipe<128, 128, false>(st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
-    return check_launch(ctx, "gemm_i8_pipe");
+      e = b_nt ? launch_pipe<128, 128, true>(dev, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y)
+               : launch_pipe<128, 128, false>(dev, st, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc, shift, relu, keep_y);
+    return check_launch(ctx, e, "gemm_i8_pipe");
   }
   dim3 grid((N + 63) / 64, (M + 63) / 64), block(256);
   if (grid.y > 65535) return fail(ctx, MIAIE_EINVAL, "gemm_i8: M too large for the 64x64 fallback");
   // vector loads need K % 16 == 0 and 16-byte aligned A (and NT B) rows
   const bool vec = K % 16 == 0 && aligned(A, 16) && lda % 16 == 0 && (!b_nt || (aligned(B, 16) && ldb % 16 == 0));
+  const int dev = ctx->device;
   if (vec) {
-    if (b_nt)
-      hipLaunchKernelGGL(gemm_i8_tile64p<true>, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy,
-                         ldc, shift, relu);
-    else
-      hipLaunchKernelGGL(gemm_i8_tile64p<false>, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy,
-                         ldc, shift, relu);
-    return check_launch(ctx, "gemm_i8_tile64p");
+    const hipError_t e =
+        b_nt ? launch<gemm_i8_tile64p<true>>(dev, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy,
+                                             ldc, shift, relu)
+             : launch<gemm_i8_tile64p<false>>(dev, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy,
+                                              ldc, shift, relu);
+    return check_launch(ctx, e, "gemm_i8_tile64p");
   }
-  if (b_nt)
-    hipLaunchKernelGGL(gemm_i8_tile64<true>, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb,
-                       ldy, ldc, shift, relu);
-  else
-    hipLaunchKernelGGL(gemm_i8_tile64<false>, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb,
-                       ldy, ldc, shift, relu);
-  return check_launch(ctx, "gemm_i8_tile64");
+  const hipError_t e =
+      b_nt ? launch<gemm_i8_tile64<true>>(dev, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc,
+                                          shift, relu)
+           : launch<gemm_i8_tile64<false>>(dev, grid, block, 0, ctx->stream, A, B, Y, C, M, N, K, lda, ldb, ldy, ldc,
+                                           shift, relu);
+  return check_launch(ctx, e, "gemm_i8_tile64");
 }
 
 }  // namespace miaie

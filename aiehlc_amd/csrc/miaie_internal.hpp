@@ -51,11 +51,13 @@ struct kernel_sig<void (*)(P...)> {
 };
 
 // Launch kernel K through the module API, with its handle looked up once per
-// device (device < 0: the current one, read on every call).  hipLaunchKernel
-// finds the kernel from its host address on every call and reports a failed
-// launch through a second call, hipGetLastError: on the host, 2.95 us per
-// launch against 2.81 us here, measured with an empty kernel of the conv's
-// 13 arguments.  The arguments are first converted to the kernel's parameter
+// device (device < 0: the current one, read on every call), and return the
+// launch's own status.  hipLaunchKernel finds the kernel from its host address
+// on every call and reports a failed launch only through hipGetLastError, the
+// thread's last error from any runtime call (a caller's earlier failure would
+// be taken for the launch's): on the host, 2.95 us per launch with that check
+// against 2.81 us here, measured with an empty kernel of the conv's 13
+// arguments.  The arguments are first converted to the kernel's parameter
 // types, since the runtime copies each by the size of its parameter.  The
 // caller has the device current (hipGetFuncBySymbol resolves on it).
 constexpr int kLaunchCacheDevices = 64;
@@ -85,11 +87,15 @@ hipError_t launch(int device, dim3 grid, dim3 block, size_t lds_bytes, hipStream
                                nullptr);
 }
 
+// A kernel as a type, for launchers that pick one of several kernels at run
+// time and launch it through launch<K>: go(kernel_t<some_kernel<...>>{}).
+template <auto K>
+struct kernel_t {
+  static constexpr auto value = K;
+};
+
 // Every entry point starts with this: non-null context, its device current.
 int enter(miaie_ctx* ctx);
-
-// Check the launch that was just queued.
-int check_launch(miaie_ctx* ctx, const char* kernel);
 
 // Entry points that wait for the device or allocate start with this: they
 // cannot be recorded into a graph.

@@ -49,12 +49,6 @@ int enter(miaie_ctx* ctx) {
   return MIAIE_OK;
 }
 
-int check_launch(miaie_ctx* ctx, const char* kernel) {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(ctx, e, kernel);
-  return MIAIE_OK;
-}
-
 int check_launch(miaie_ctx* ctx, hipError_t e, const char* kernel) {
   if (e != hipSuccess) return hip_fail(ctx, e, kernel);
   return MIAIE_OK;
@@ -410,10 +404,11 @@ extern "C" int miaie_copy_d2d(miaie_ctx* ctx, void* dst, const void* src, size_t
   if (blocks > 8192) blocks = 8192;
   if (blocks < (ntail + 255) / 256) blocks = (ntail + 255) / 256;
   if (blocks == 0) blocks = 1;
-  hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream,
-                     static_cast<v4i*>(dst), static_cast<const v4i*>(src), nvec,
-                     static_cast<uint8_t*>(dst) + done, static_cast<const uint8_t*>(src) + done, ntail);
-  return check_launch(ctx, "copy_kernel");
+  const hipError_t e = launch<copy_kernel>(ctx->device, dim3((unsigned)blocks), dim3(256), 0, ctx->stream,
+                                           static_cast<v4i*>(dst), static_cast<const v4i*>(src), nvec,
+                                           static_cast<uint8_t*>(dst) + done, static_cast<const uint8_t*>(src) + done,
+                                           ntail);
+  return check_launch(ctx, e, "copy_kernel");
 }
 
 // ---------------------------------------------------------------- waits
@@ -479,8 +474,8 @@ extern "C" int miaie_fill_i8(miaie_ctx* ctx, int8_t* dst, size_t n, uint64_t ten
   const size_t threads = (n + 15) / 16;
   const size_t blocks = (threads + 255) / 256;
   if (blocks > 0x7FFFFFFF) return fail(ctx, MIAIE_EINVAL, "miaie_fill_i8: n too large");
-  hipLaunchKernelGGL(fill_i8_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, dst, n, state0);
-  return check_launch(ctx, "fill_i8_kernel");
+  return check_launch(ctx, launch<fill_i8_kernel>(ctx->device, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, dst, n, state0),
+                      "fill_i8_kernel");
 }
 
 extern "C" const char* miaie_version(void) { return "miaie 0.1 (gfx950)"; }

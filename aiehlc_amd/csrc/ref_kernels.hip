@@ -144,8 +144,7 @@ extern "C" int miaie_mm_window_i32(miaie_ctx* ctx, const int32_t* in, int32_t* o
   if (n < 1 || n > 4096) return fail(ctx, MIAIE_EINVAL, "miaie_mm_window_i32: n=%d outside [1, 4096]", n);
   if (!aligned(in, 4) || !aligned(out, 4)) return fail(ctx, MIAIE_EINVAL, "miaie_mm_window_i32: misaligned buffer");
   dim3 grid((n + WT - 1) / WT, (n + WT - 1) / WT);
-  hipLaunchKernelGGL(mm_window_i32, grid, dim3(256), 0, ctx->stream, in, out, n);
-  return check_launch(ctx, "mm_window_i32");
+  return check_launch(ctx, launch<mm_window_i32>(ctx->device, grid, dim3(256), 0, ctx->stream, in, out, n), "mm_window_i32");
 }
 
 extern "C" int miaie_perf_window_u32(miaie_ctx* ctx, const uint32_t* in, uint32_t* out, int n) {
@@ -159,13 +158,12 @@ extern "C" int miaie_dot_u8_probe(miaie_ctx* ctx, const uint32_t* in, uint32_t* 
   MIAIE_CHECK_NOT_NULL(ctx, in);
   MIAIE_CHECK_NOT_NULL(ctx, out);
   if (!aligned(in, 4) || !aligned(out, 4)) return fail(ctx, MIAIE_EINVAL, "miaie_dot_u8_probe: misaligned buffer");
-  hipLaunchKernelGGL(dot_probe_init, dim3(1), dim3(64), 0, ctx->stream, in, out);
-  rc = check_launch(ctx, "dot_probe_init");
+  rc = check_launch(ctx, launch<dot_probe_init>(ctx->device, dim3(1), dim3(64), 0, ctx->stream, in, out), "dot_probe_init");
   if (rc) return rc;
   // 1024 workgroups x 4 waves: per-wave group counts stay far below the
   // int32 accumulator range (dot <= 512, groups per wave <= 3*2^32/2^22).
-  hipLaunchKernelGGL(dot_probe_mfma, dim3(1024), dim3(256), 0, ctx->stream, in, out);
-  return check_launch(ctx, "dot_probe_mfma");
+  return check_launch(ctx, launch<dot_probe_mfma>(ctx->device, dim3(1024), dim3(256), 0, ctx->stream, in, out),
+                      "dot_probe_mfma");
 }
 
 extern "C" int miaie_mm_square_u64(miaie_ctx* ctx, const uint64_t* in, uint64_t* out, int n, int batch,
@@ -179,8 +177,8 @@ extern "C" int miaie_mm_square_u64(miaie_ctx* ctx, const uint64_t* in, uint64_t*
   if (iters < 1 || iters > (1ull << 20) || iters * (uint64_t)n * n * n > (1ull << 34))
     return fail(ctx, MIAIE_EINVAL, "miaie_mm_square_u64: iters must be in [1, 2^20] with iters*n^3 <= 2^34");
   if (!aligned(in, 8) || !aligned(out, 8)) return fail(ctx, MIAIE_EINVAL, "miaie_mm_square_u64: misaligned buffer");
-  hipLaunchKernelGGL(mm_square_u64, dim3(batch), dim3(64), 0, ctx->stream, in, out, n, iters);
-  return check_launch(ctx, "mm_square_u64");
+  return check_launch(ctx, launch<mm_square_u64>(ctx->device, dim3(batch), dim3(64), 0, ctx->stream, in, out, n, iters),
+                      "mm_square_u64");
 }
 
 extern "C" int miaie_chain_add_i32(miaie_ctx* ctx, const int32_t* in, int32_t* out, int len, const int32_t* addends,
@@ -195,6 +193,7 @@ extern "C" int miaie_chain_add_i32(miaie_ctx* ctx, const int32_t* in, int32_t* o
   ChainArgs args{};
   for (int s = 0; s < nstages; ++s) args.add[s] = addends[s];
   const int blocks = (len + 255) / 256 < 1024 ? (len + 255) / 256 : 1024;
-  hipLaunchKernelGGL(chain_add_i32, dim3(blocks), dim3(256), 0, ctx->stream, in, out, len, args, nstages);
-  return check_launch(ctx, "chain_add_i32");
+  return check_launch(ctx, launch<chain_add_i32>(ctx->device, dim3(blocks), dim3(256), 0, ctx->stream, in, out, len, args,
+                                                 nstages),
+                      "chain_add_i32");
 }
