@@ -621,6 +621,38 @@ def test_argument_errors(ctx):
     d.free()
 
 
+def test_launch_status_ignores_earlier_runtime_errors(ctx):
+    """A failed HIP call of the caller's own (here hipSetDevice on a device
+    that does not exist) before an entry point does not make its launches
+    report a failure: each launch's status is the launch's own."""
+    import ctypes
+
+    _say("launch status after a caller's failed runtime call")
+    hip = ctypes.CDLL("libamdhip64.so")
+    count = ctypes.c_int()
+    assert hip.hipGetDeviceCount(ctypes.byref(count)) == 0
+    M = N = K = 256
+    rng = np.random.default_rng(5)
+    A = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    dA, dB, dY = ctx.upload(A), ctx.upload(B), ctx.empty((M, N), np.int8)
+    X = rng.integers(-128, 128, size=(1, 8, 8, 64), dtype=np.int8)
+    Wt = rng.integers(-128, 128, size=(64, 3, 3, 64), dtype=np.int8)
+    sh = np.full(64, 9, dtype=np.uint8)
+    dX, dW, dS, dC = ctx.upload(X), ctx.upload(Wt), ctx.upload(sh), ctx.empty((1, 8, 8, 64), np.int8)
+    for call in (lambda: ctx.call_status("miaie_gemm_i8_rq", dA.ptr, dB.ptr, dY.ptr, M, N, K, 10, 0, None, mi.B_NN),
+                 lambda: ctx.call_status("miaie_conv2d_i8_nhwc", dX.ptr, dW.ptr, dS.ptr, dC.ptr, 1, 8, 8, 64, 64, 3, 3,
+                                         1, 1)):
+        assert hip.hipSetDevice(count.value + 7) != 0  # the caller's own failed call
+        assert call() == mi.MIAIE_OK, ctx.last_error()
+    ctx.wait(10_000)
+    assert np.array_equal(ctx.download(dY), oracle.requant(oracle.gemm_i8(A, B), 10))
+    assert np.array_equal(ctx.download(dC), oracle.conv2d_nhwc_i8(X, Wt, sh, 1, 1))
+    for b in (dA, dB, dY, dX, dW, dS, dC):
+        b.free()
+    hip.hipGetLastError()  # clear the planted error for whatever runs next
+
+
 def test_wait_deadline(ctx):
     """miaie_wait returns MIAIE_ETIMEDOUT when the deadline passes first and OK once drained."""
     _say("wait deadline")
