@@ -310,6 +310,8 @@ CONV_SHAPES = [
     (1, 6, 60, 128, 96, 3, 3, 1, 2),  # row-block 4 x 32 at Cin 128, pad 2
     (1, 10, 64, 128, 128, 3, 3, 1, 1),  # row-block 4 x 32 at Cin 128, four channel blocks, last block half outside
     (2, 11, 40, 32, 64, 3, 3, 1, 1),  # row-block 4 x 32 at Cin 32, Cout 64, last block 3 rows
+    (1, 8, 30, 64, 128, 3, 3, 1, 1),  # Ho = 8, the first height on 4 x 32 at Cout % 64 == 0: two whole row blocks
+    (3, 8, 66, 32, 64, 3, 3, 1, 1),   # 4 x 32, Wo 66: two column blocks (the second 2 columns wide), N % 8 != 0 grid
     (1, 5, 9, 96, 64, 3, 3, 1, 1),    # Cin 96: implicit-GEMM kernel
     (1, 8, 8, 256, 64, 3, 3, 1, 1),   # chunked row-block kernel: four 64-channel chunks, one workgroup
     (1, 16, 16, 256, 64, 3, 3, 2, 1),  # taps kernel (LDS-staged), stride 2: one tile split 4 ways over k (partials + reduce)
