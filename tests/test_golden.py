@@ -1,12 +1,18 @@
 """Committed fixtures (tests/golden/golden.npz, written by numpy integer
 arithmetic in tests/golden/make_golden.py) checked against the CPU oracle
-(CPU) and against the gfx950 kernels through the C ABI (GPU)."""
+(CPU) and against the gfx950 kernels through the C ABI (GPU); the recorded
+synthetic inputs of the benchmark configurations (tests/golden/
+synthetic_manifest.json) against the host generators (CPU) and the device
+fill (GPU)."""
+import hashlib
+import json
 import os
 
 import numpy as np
 import pytest
 
 import oracle
+from aiehlc_amd import synth
 
 G = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz"))
 
@@ -35,6 +41,40 @@ def test_oracle_conv_and_mlp_fixtures():
     assert np.array_equal(oracle.conv2d_nhwc_i8(G["conv_X"], G["conv_W"], G["conv_shifts"], 1, 1), G["conv_Y"])
     Y, H = oracle.mlp_i8(G["mlp_X"], G["mlp_W1"], G["mlp_W2"], 11, 12, want_h=True)
     assert np.array_equal(H, G["mlp_H"]) and np.array_equal(Y, G["mlp_Y"])
+
+
+# ------------------------------------------------- CPU: the benchmark's synthetic inputs
+MANIFEST = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                       "synthetic_manifest.json")))
+
+
+def _sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def _int8_entries():
+    for c, tensors in sorted(MANIFEST["configs"].items()):
+        for name, t in sorted(tensors.items()):
+            if isinstance(t, dict) and t.get("dtype") == "int8":
+                yield c, name, t
+
+
+@pytest.mark.parametrize("c,name,t", list(_int8_entries()), ids=lambda v: v if isinstance(v, str) else "")
+def test_synthetic_int8_inputs_match_the_manifest(c, name, t):
+    """The numpy generator and the C oracle's generator both reproduce the
+    recorded bytes of every int8 benchmark input (tests/golden/make_manifest.py)."""
+    shape = tuple(t["shape"])
+    assert _sha(synth.int8(shape, t["stream"])) == t["sha256"], (c, name)
+    if int(np.prod(shape)) <= (1 << 24):
+        assert _sha(oracle.fill_i8(int(np.prod(shape)), t["stream"])) == t["sha256"], (c, name)
+
+
+def test_synthetic_shifts_and_bf16_match_the_manifest():
+    cfg = MANIFEST["configs"]
+    assert synth.shifts(64, 7).tolist() == cfg["4"]["shifts"]["values"]
+    assert oracle.fill_shift(64, 7).tolist() == cfg["4"]["shifts"]["values"]
+    for name, sid in (("A", 1), ("B", 2)):
+        assert synth.bf16_normal((16,), sid, 1.0 / np.sqrt(8192)).tolist() == cfg["3"][name]["first16_bits"]
 
 
 # ---------------------------------------------------------------- GPU: kernels vs fixtures
@@ -80,3 +120,19 @@ def test_gpu_conv_and_mlp_fixtures(ctx):
     ctx.wait(10_000)
     assert np.array_equal(ctx.download(dH), G["mlp_H"])
     assert np.array_equal(ctx.download(dYm), G["mlp_Y"])
+
+
+@pytest.mark.gpu
+def test_gpu_fill_matches_the_manifest(ctx):
+    """miaie_fill_i8 on the device writes the recorded bytes of config 2's A
+    and B and config 4's X and W, the inputs bench.py generates on the device."""
+    print("[case] device fill vs manifest", flush=True)
+    cfg = MANIFEST["configs"]
+    for c, name in (("2", "A"), ("2", "B"), ("4", "X"), ("4", "W")):
+        t = cfg[c][name]
+        n = int(np.prod(t["shape"]))
+        d = ctx.empty((n,), np.int8)
+        ctx.fill_i8(d, n, t["stream"])
+        ctx.wait(10_000)
+        assert _sha(ctx.download(d)) == t["sha256"], (c, name)
+        d.free()
