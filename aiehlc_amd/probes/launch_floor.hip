@@ -13,10 +13,12 @@
 //                       whole batch was queued before the wait ended
 // When host_issue_us exceeds device_us, a host thread issuing one launch
 // after another is what limits the back-to-back rate, not the device.
+// host_launch_paths: the host's time per launch through each launch API.
 //
 // Prints one JSON object.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -100,6 +102,60 @@ void run(hipStream_t st, int* out, int blocks, int iters, const char* name, bool
   CHECK(hipEventDestroy(e1));
 }
 
+// An empty kernel with the conv2d_i8_rows argument list (13 arguments).
+__global__ __launch_bounds__(512) void empty13(const int8_t* X, const int8_t* W, const uint8_t* s, int8_t* Y, int H,
+                                               int Wd, int Cout, int pad, int Ho, int Wo, int xg, int ncb,
+                                               unsigned long long* probe) {
+  if (H == 0x5eed && threadIdx.x == 0) Y[blockIdx.x] = (int8_t)Wd;
+}
+
+// Host time per launch of the conv grid's empty kernel through the ways a
+// library can launch it: hipLaunchKernelGGL alone, with the hipGetLastError
+// check, with hipSetDevice or hipGetDevice in front (what each entry point
+// does to make its device current), and hipModuleLaunchKernel with a handle
+// looked up once (hipGetFuncBySymbol) or hipExtLaunchKernel.  Each figure
+// is the median of 9 loops of `iters` launches, the host's clock around the
+// loop (the device runs these launches faster than the host issues them).
+void launch_paths(hipStream_t st, int8_t* y, int iters) {
+  const dim3 grid(8, 14, 2), blk(512);
+  const int8_t* X = nullptr;
+  const int8_t* W = nullptr;
+  const uint8_t* S = nullptr;
+  int H = 56, Wd = 56, Cout = 64, pad = 1, Ho = 56, Wo = 56, xg = 1, ncb = 1;
+  unsigned long long* P = nullptr;
+  hipFunction_t f;
+  CHECK(hipGetFuncBySymbol(&f, reinterpret_cast<const void*>(&empty13)));
+  void* args[] = {&X, &W, &S, &y, &H, &Wd, &Cout, &pad, &Ho, &Wo, &xg, &ncb, &P};
+  auto ggl = [&]() { hipLaunchKernelGGL(empty13, grid, blk, 0, st, X, W, S, y, H, Wd, Cout, pad, Ho, Wo, xg, ncb, P); };
+  auto time = [&](auto fn) {
+    double t[9];
+    for (int r = 0; r < 9; ++r) {
+      CHECK(hipStreamSynchronize(st));
+      const auto t0 = clk::now();
+      for (int i = 0; i < iters; ++i) fn();
+      t[r] = us_since(t0) / iters;
+      CHECK(hipStreamSynchronize(st));
+    }
+    std::sort(t, t + 9);
+    return t[4];
+  };
+  int dev = 0;
+  CHECK(hipGetDevice(&dev));
+  const double a = time(ggl);
+  const double b = time([&]() { ggl(); (void)hipGetLastError(); });
+  const double c = time([&]() { (void)hipSetDevice(dev); ggl(); (void)hipGetLastError(); });
+  const double d = time([&]() { int cur; (void)hipGetDevice(&cur); if (cur != dev) (void)hipSetDevice(dev); ggl(); (void)hipGetLastError(); });
+  const double e = time([&]() { (void)hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, blk.x, 1, 1, 0, st, args, nullptr); });
+  const double g = time([&]() { int cur; (void)hipGetDevice(&cur); (void)hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, blk.x, 1, 1, 0, st, args, nullptr); });
+  const double h = time([&]() { (void)hipExtLaunchKernel(reinterpret_cast<const void*>(&empty13), grid, blk, args, 0, st, nullptr, nullptr, 0); });
+  CHECK(hipGetLastError());
+  printf("  \"host_launch_paths\": {\"kernel\": \"empty, 13 arguments, conv grid 224 x 512\", \"launches\": %d, "
+         "\"us\": {\"hipLaunchKernelGGL\": %.3f, \"+hipGetLastError\": %.3f, \"hipSetDevice+GGL+hipGetLastError\": %.3f, "
+         "\"hipGetDevice+GGL+hipGetLastError\": %.3f, \"hipModuleLaunchKernel_cached_handle\": %.3f, "
+         "\"hipGetDevice+hipModuleLaunchKernel_cached_handle\": %.3f, \"hipExtLaunchKernel\": %.3f}}\n",
+         iters, a, b, c, d, e, g, h);
+}
+
 int main(int argc, char** argv) {
   const int iters = argc > 1 ? atoi(argv[1]) : 5000;
   int* out = nullptr;
@@ -111,7 +167,8 @@ int main(int argc, char** argv) {
   run<56576, 512>(st, out, 224, iters, "conv2d_rows_grid", false);
   // gemm_i8_pipe16<256,256> at 4096^3: 256 workgroups of 256 threads, 160 KiB of LDS
   run<163840, 256>(st, out, 256, iters, "gemm_256x256_grid", false);
-  run<0, 64>(st, out, 1, iters, "one_wave", true);
+  run<0, 64>(st, out, 1, iters, "one_wave", false);
+  launch_paths(st, reinterpret_cast<int8_t*>(out), iters < 500 ? iters : 500);
   printf("}\n");
   CHECK(hipFree(out));
   CHECK(hipStreamDestroy(st));

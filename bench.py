@@ -24,7 +24,8 @@ Also in the line (not the headline):
                          issue time per launch, and the device's time per
                          launch with the queue already filled; the conv line
                          carries the device figure as its floor and the time
-                         above it
+                         above it; host_launch_paths: the host's time per
+                         launch through each HIP launch API
   extras.reference_flow_16x16, extras.reference_flow_8x8
                          the reference's own timed example flow (aieml_mm.cc:
                          an int32 tile moved in, run, waited for, moved out)
