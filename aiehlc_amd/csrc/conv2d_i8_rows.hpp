@@ -135,12 +135,17 @@ constexpr int PROBE_WORDS = 6;
 // image-per-XCD grid.  ncb: blocks of PB output columns per row (rows wider
 // than PB are split; the row-block grid index counts row block x ncb +
 // column block).  probe: PROBE_WORDS words per wave (TIMED only).
+// The arguments fit the 14 dwords that arrive in SGPRs at wave launch (four
+// pointers, then six ints with no alignment gap; the output size is
+// H + 2 pad - 2 by W + 2 pad - 2), so nothing waits for a load from the
+// argument segment; probe (TIMED only) comes after them.
 template <int R, int S, int CIN, int ROWS, int WCO, bool TIMED>
 __global__ __launch_bounds__(512) void conv2d_i8_rows(const int8_t* __restrict__ X, const int8_t* __restrict__ W,
                                                       const uint8_t* __restrict__ shifts, int8_t* __restrict__ Y,
-                                                      int H, int Wd, int Cout, int pad, int Ho, int Wo, int xg,
-                                                      int ncb, unsigned long long* __restrict__ probe) {
+                                                      int H, int Wd, int pad, int xg, int ncb, int Cout,
+                                                      unsigned long long* __restrict__ probe) {
   using G = RowsGeom<R, S, CIN, ROWS, WCO>;
+  const int Ho = H + 2 * pad - (R - 1), Wo = Wd + 2 * pad - (S - 1);
   __shared__ __attribute__((aligned(16))) int8_t smem[G::LDS];
   unsigned long long t0 = 0, r0 = 0;
   if constexpr (TIMED) {
@@ -309,7 +314,7 @@ inline hipError_t launch_rows_as(int device, hipStream_t st, const int8_t* X, co
   const bool by_xcd = N % 8 == 0 && rbs <= 65535 && (size_t)(N / 8) * cbs <= 65535;
   const dim3 grid = by_xcd ? dim3(8, rbs, (unsigned)(N / 8) * cbs) : dim3(rbs, cbs, (unsigned)N);
   return launch<conv2d_i8_rows<3, 3, CIN, ROWS, WCO, TIMED>>(device, grid, dim3(512), 0, st, X, W, shifts, Y, H, Wd,
-                                                             Cout, pad, Ho, Wo, by_xcd ? N / 8 : 0, ncb, probe);
+                                                             pad, by_xcd ? N / 8 : 0, ncb, Cout, probe);
 }
 
 
