@@ -382,6 +382,48 @@ def test_conv2d_i8_random_shapes(ctx, shape):
     assert np.array_equal(ctx.download(dY), oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad))
 
 
+def _random_rows_cases(n=48, seed=20261202):
+    """3x3 stride-1 layers for the row-block kernels: Cin 32/64/128, Cout a
+    multiple of 32 (both workgroup shapes), heights across the 4-row block
+    boundary, widths over one to three 64-column blocks, batch sizes on both
+    grid forms, pads 0-2, planned for 1 to 256 CUs."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        Cin = int(rng.choice([32, 64, 128]))
+        Cout = int(rng.choice([32, 64, 96, 128, 160, 256]))
+        H, W = int(rng.integers(3, 22)), int(rng.integers(3, 150))
+        N, pad = int(rng.choice([1, 2, 3, 8, 9, 16])), int(rng.integers(0, 3))
+        if N * H * W * Cout * Cin > 6e8:
+            N = 1
+        cases.append(((N, H, W, Cin, Cout, 3, 3, 1, pad), int(rng.choice([256, 256, 64, 8, 1]))))
+    return cases
+
+
+@pytest.mark.parametrize("shape,cus", _random_rows_cases())
+def test_conv2d_i8_rows_random(ctx, shape, cus):
+    """Seeded random layers on the row-block kernels (4 x 32 and 2 x 64
+    workgroups, and the chunked kernel where a CU count makes it the
+    choice), per-channel shifts over [0, 31], bit-exact against the oracle."""
+    N, H, W, Cin, Cout, R, S, stride, pad = shape
+    _say("conv2d rows random", shape, "cus", cus)
+    rng = np.random.default_rng(sum(shape) * 31 + cus)
+    X = rng.integers(-128, 128, size=(N, H, W, Cin), dtype=np.int8)
+    Wt = rng.integers(-128, 128, size=(Cout, R, S, Cin), dtype=np.int8)
+    sh = rng.integers(0, 32, size=Cout, dtype=np.uint8)
+    Ho, Wo = H + 2 * pad - 2, W + 2 * pad - 2
+    prev = ctx.plan_set_cus(cus)
+    try:
+        dX, dW, dS = ctx.upload(X), ctx.upload(Wt), ctx.upload(sh)
+        dY = ctx.empty((N, Ho, Wo, Cout), np.int8)
+        ctx.conv2d_i8_nhwc(dX, dW, dS, dY, N, H, W, Cin, Cout, R, S, stride, pad)
+        ctx.wait(60_000)
+        Yg = ctx.download(dY)
+    finally:
+        ctx.plan_set_cus(prev)
+    assert np.array_equal(Yg, oracle.conv2d_nhwc_i8(X, Wt, sh, stride, pad))
+
+
 @pytest.mark.parametrize("shape", [
     (1, 9, 70, 256, 128, 3, 3, 2, 1),   # stride 2: 2 pixel tiles, the last partial
     (2, 7, 7, 256, 256, 5, 5, 1, 2),    # 5x5: one partial pixel tile, two channel tiles
